@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""Benchmark of the decoder hot path on one MI355X.
+
+Workload (the headline "decode ms/token"): full 28-layer greedy decode of a
+random-init Qwen3-0.6B-shaped model (d=1024, 16Q/8KV heads x 128, FFN 3072,
+vocab 151936), FP16 layer weights, INT8 lm_head with per-column fp32 scales,
+RoPE theta 1e6 split-half, fp16 KV cache prefilled to 512 positions with
+N(0,1) values; each timed step decodes one token with the argmax fed back on
+the device.  A "step" is one token.  value = tokens/s over the timed steps
+(host wall clock around the whole timed loop, GPU synchronised on both
+sides).
+
+Also reported: the M=60 INT8 batch prefill (28 layers, 60 tokens from an
+empty cache), the per-projection GEMV bandwidth, the roofline of the dominant
+kernel (timed with HIP events on the decoder's stream), and the oracle (the
+scalar C restatement of the reference CPU path) timed on this host on a
+bounded sample of the same decode workload.
+
+Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "rknn-matmul-parallel_amd")
+sys.path.insert(0, PKG)
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+KV_PREFILL = 512
+START_TOKEN = 151644
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_dir(mdx, tag: str, cfg, quant: int, seed: int) -> str:
+    base = os.environ.get("MDX_BENCH_DIR") or os.path.join(tempfile.gettempdir(), "mdx_bench")
+    path = os.path.join(base, tag)
+    marker = os.path.join(path, ".complete")
+    if not os.path.exists(marker):
+        t0 = time.time()
+        os.makedirs(base, exist_ok=True)
+        mdx.write_model(path, cfg, quant, seed)
+        open(marker, "w").close()
+        log(f"wrote {tag} in {time.time() - t0:.1f}s")
+    return path
+
+
+def step_bytes(d: dict, positions: list[int]) -> float:
+    """Algorithmic HBM bytes of one decode step (weights + lm_head + KV), mean over positions."""
+    h, qd, kvd, F, L, V = d["hidden_dim"], d["num_q_heads"] * d["head_dim"], \
+        d["num_kv_heads"] * d["head_dim"], d["ffn_dim"], d["num_layers"], d["vocab_size"]
+    layer_w = 2.0 * (h * (qd + 2 * kvd) + qd * h + 2 * h * F + F * h)
+    norms = 4.0 * (2 * h + 2 * d["head_dim"])
+    lm = V * h * 1.0 + V * 4.0
+    kv = np.mean([L * (p + 1) * kvd * 2 * 2.0 for p in positions])
+    return L * (layer_w + norms) + lm + kv + 4.0 * h
+
+
+def cpu_info() -> dict:
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count()}
+
+
+def run_cpu_baseline(path: str, d: dict, budget_s: float) -> dict:
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    t0 = time.time()
+    m = orc.Model(path, d, 0, KV_PREFILL + 64, kv_fp16=True)
+    m.kv_fill_normal(KV_PREFILL, 1003)
+    log(f"oracle loaded in {time.time() - t0:.1f}s")
+    n, tok, t_start = 0, START_TOKEN, time.perf_counter()
+    while True:
+        tok, _ = m.step(tok)
+        n += 1
+        el = time.perf_counter() - t_start
+        if el >= budget_s or n >= 64:
+            break
+    m.close()
+    info = cpu_info()
+    return {"value": round(n / el, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "ms_per_token": round(el / n * 1000, 2),
+            "sample": f"{n} greedy decode steps of the same 28-layer fp16/int8-lm_head model at KV "
+                      f"{KV_PREFILL}..{KV_PREFILL + n} (oracle: scalar C restatement of the reference "
+                      f"CPU path, gcc -O3, 1 thread), {el:.1f} s",
+            **info}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle decode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the decoder on a single MI355X and has "
+              "no multi-GPU path (see DESIGN.md for how it would shard); use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import mdx_lib as mdx
+    if mdx.device_count() <= 0:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+
+    d = dict(hidden_dim=1024, num_q_heads=16, num_kv_heads=8, head_dim=128, ffn_dim=3072,
+             num_layers=28, vocab_size=151936, max_seq_len=4096, rms_eps=1e-6, rope_theta=1e6,
+             tie_word_embeddings=1, has_qk_norm=1, rope_style=1, max_batch_prefill=64)
+    cfg = mdx.qwen3_0_6b_config(name="qwen3-0.6b-synthetic", **d)
+    max_seq = KV_PREFILL + max(args.steps, args.warmup) + 8
+
+    # ---- decode (config: 28-layer greedy, FP16 layers + INT8 lm_head, KV 512) ----
+    path16 = model_dir(mdx, "decode_fp16_seed1003", cfg, 0, 1003)
+    t0 = time.time()
+    dec = mdx.Decoder(path16, cfg, "fp16", max_seq)
+    log(f"decoder created in {time.time() - t0:.1f}s")
+    dec.kv_fill_normal(KV_PREFILL, 1003)
+    dec.generate_greedy(START_TOKEN, args.warmup)
+    dec.kv_fill_normal(KV_PREFILL, 1003)
+    t0 = time.perf_counter()
+    toks, dev_ms = dec.generate_greedy(START_TOKEN, args.steps)
+    wall_s = time.perf_counter() - t0
+    ms_per_step = wall_s * 1000.0 / args.steps
+    positions = list(range(KV_PREFILL, KV_PREFILL + args.steps))
+    bytes_step = step_bytes(d, positions)
+    log(f"decode: {ms_per_step * 1000:.1f} us/token wall, {dev_ms * 1000 / args.steps:.1f} us/token device")
+
+    # API-level latency: matmul_decoder_step with logits copied to the host each token
+    dec.kv_fill_normal(KV_PREFILL, 1003)
+    logits = np.empty(d["vocab_size"], np.float32)
+    tok, t0 = START_TOKEN, time.perf_counter()
+    n_api = min(args.steps, 32)
+    for _ in range(n_api):
+        tok, _ = dec.step(tok)
+    api_ms = (time.perf_counter() - t0) * 1000.0 / n_api
+
+    # per-projection kernels (each launch cycles through the 28 layers' weights)
+    kernels = {}
+    for name, per_step in (("qkv", 28), ("o", 28), ("gate_up", 28), ("down", 28), ("lm_head", 1)):
+        iters = 280 if per_step == 28 else 40
+        dec.time_projection(name, 28)
+        us, b = dec.time_projection(name, iters)
+        kernels[name] = {"avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
+                         "per_step_us": round(us * per_step, 1)}
+    dom = max(kernels, key=lambda k: kernels[k]["per_step_us"])
+    kd = kernels[dom]
+    kernel_names = {"qkv": "k_gemv<KF16> fused RMSNorm + merged QKV projection",
+                    "o": "k_gemv<KF16> o_proj + residual add",
+                    "gate_up": "k_gemv<KF16> fused RMSNorm + gate/up + SwiGLU",
+                    "down": "k_gemv<KF16> down_proj + residual add",
+                    "lm_head": "k_gemv<KI8> fused final RMSNorm + INT8 lm_head + argmax partials"}
+    dec.close()
+
+    # ---- batch prefill M=60 through 28 INT8 layers ----
+    prefill = None
+    if not args.no_prefill:
+        path8 = model_dir(mdx, "prefill_int8_seed1004", cfg, 1, 1004)
+        dec8 = mdx.Decoder(path8, cfg, "int8", 128)
+        emb = mdx.synth_fill_normal(60 * 1024, mdx.synth_seed(1004, "prefill/emb")).reshape(60, 1024)
+        dec8.time_prefill(emb, 3)
+        pms = dec8.time_prefill(emb, 20)
+        layer_bytes = 28 * (1.0 * (1024 * 4096 + 2048 * 1024 + 2 * 1024 * 3072 + 3072 * 1024)
+                            + 4.0 * (4096 + 1024 + 6144 + 1024) + 4.0 * (2 * 1024 + 256))
+        flops = 2.0 * 60 * 28 * (1024 * 4096 + 2048 * 1024 + 2 * 1024 * 3072 + 3072 * 1024)
+        dec8.close()
+        prefill = {"ms": round(pms, 4), "tokens": 60,
+                   "hbm_frac_layers": round(layer_bytes / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "mfma_frac_layers": round(flops / (pms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
+                   "note": "28 INT8 layers, causal GQA over 60 positions, device time (HIP events)"}
+        log(f"prefill M=60: {pms:.3f} ms")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = run_cpu_baseline(path16, d, args.cpu_budget)
+        log(f"cpu baseline: {cpu['ms_per_token']} ms/token")
+
+    line = {
+        "metric": "decode ms/token + M=60 prefill ms, 0.6B/28L shape; GEMV HBM GB/s",
+        "value": round(args.steps / wall_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random-init Qwen3-0.6B-shaped weights and N(0,1) KV)",
+        "config": {"workload": "28-layer greedy decode, fp16 layers + int8 lm_head, fp16 KV 512->576, "
+                               "1 token per step, argmax fed back on device",
+                   "hidden": 1024, "heads": "16q/8kv x128", "ffn": 3072, "vocab": 151936,
+                   "kv_start": KV_PREFILL, "start_token": START_TOKEN},
+        "roofline": {"bound": "hbm", "kernel": kernel_names[dom],
+                     "achieved": kd["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kd["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": kd["bytes"], "avg_us": kd["avg_us"]},
+        "step_roofline": {"bytes_per_step": bytes_step,
+                          "achieved_GBps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
+                          "frac": round(bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "device_us_per_step": round(dev_ms * 1000 / args.steps, 2)},
+        "api_step_ms": round(api_ms, 4),
+        "kernels": kernels,
+        "prefill_m60": prefill,
+        "cpu_baseline": cpu,
+        "tokens_head": toks[:8],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

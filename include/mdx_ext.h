@@ -1,0 +1,126 @@
+/*
+ * mdx_ext.h — additive C entry points of the MI355X decoder library.
+ *
+ * None of these exist in the reference; they sit beside the drop-in ABI
+ * (matmul_decoder.h, rknn_matmul_parallel.h) and never change its
+ * behaviour.  They serve three groups of callers:
+ *   - test hooks the reference API lacks (KV fill/read, last-token logits
+ *     after a batch prefill);
+ *   - single-kernel entry points so parity tests can check one projection,
+ *     one attention call or one GEMM against the oracle;
+ *   - device-resident loops and timers for measurement (greedy decode with
+ *     the token fed back on the device, GEMV bandwidth timing).
+ * Every function returns 0 (or a token id) on success and a negative
+ * MatmulDecoderError code on failure.
+ */
+#ifndef MDX_EXT_H
+#define MDX_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "matmul_decoder.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library build information: "<version> gfx950". */
+const char* mdx_version(void);
+/* Number of visible GPUs (0 when the HIP runtime finds none). */
+int mdx_device_count(void);
+/* Last HIP runtime message recorded by the library (thread-local). */
+const char* mdx_last_error(void);
+
+/* matmul_decoder_step with the lm_head and argmax but without copying the
+ * logits to the host (the pybind step_get_token path). */
+int mdx_step_token(MatmulDecoderContext* ctx, int token_id, const float* embedding);
+
+/* ---- test hooks on a decoder context ---- */
+
+/* Fill KV rows [0, n_pos) of every layer with N(0,1) values rounded to fp16
+ * (streams "kv/k/LL" and "kv/v/LL" of mdx_synth_fill_normal, seed `seed`)
+ * and set the sequence length to n_pos. */
+int mdx_kv_fill_normal(MatmulDecoderContext* ctx, int n_pos, uint64_t seed);
+/* Read KV rows [pos0, pos0+n) of one layer as fp32 [n][kv_heads*head_dim]. */
+int mdx_kv_read(const MatmulDecoderContext* ctx, int layer, int pos0, int n, float* k, float* v);
+/* Batch prefill of M rows, then final norm + lm_head on the last row
+ * (BASELINE config 4's "lm_head on the last token only").  Writes logits
+ * when non-NULL and returns the argmax. */
+int mdx_prefill_logits(MatmulDecoderContext* ctx, const float* embeddings, int M, float* logits);
+/* n_steps greedy tokens starting from token `first_token`, with each argmax
+ * fed back on the device (no host round trip between steps).  Tokens go to
+ * out_tokens[n_steps]; *device_ms (optional) receives the GPU time of the
+ * whole loop.  Equivalent to n_steps calls of matmul_decoder_step with the
+ * previous result as token_id. */
+int mdx_generate_greedy(MatmulDecoderContext* ctx, int first_token, int n_steps, int* out_tokens,
+                        float* device_ms);
+/* Average device microseconds of one launch of a layer projection kernel
+ * ("qkv", "o", "gate_up", "down", "lm_head"), timed with HIP events over
+ * `iters` launches cycling through all layers (distinct weights).  *bytes
+ * receives the algorithmic HBM bytes of one launch. */
+int mdx_time_projection(MatmulDecoderContext* ctx, const char* which, int iters, float* avg_us,
+                        double* bytes);
+/* Device milliseconds of one M-row batch prefill through all layers (timed
+ * with HIP events, KV position restored afterwards). */
+int mdx_time_prefill(MatmulDecoderContext* ctx, const float* embeddings, int M, int iters,
+                     float* avg_ms);
+
+/* ---- single-kernel entry points (weights in the on-disk layout) ---- */
+
+/* kind: 0 fp16 [K,N] (uint16 bits), 1 int8 [K,N], 2 int4 [K,N/2] (byte
+ * (k,j): column 2j in the low nibble, 2j+1 in the high nibble), 3 fp32
+ * rows [N,K] with fp32 x (the CPU GEMV), 4 fp16 rows [N,K] with fp32 x.
+ * scales[N] may be NULL.  y[N] fp32 = fp16(x) . W (x scale). */
+int mdx_debug_gemv(int kind, int K, int N, const void* w, const float* scales, const float* x,
+                   float* y);
+/* M-row MFMA projection, M <= 64: y[M,N] = fp16(x[M,K]) . W (x scale). */
+int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* scales,
+                   const float* x, float* y);
+/* One decode attention: q fp32 [nq*hd], cache rows fp16 bits [L][nkv*hd],
+ * out fp32 [nq*hd] (the fp16 value the kernel stores, widened). */
+int mdx_debug_attn_decode(int nq, int nkv, int hd, int L, const float* q, const uint16_t* k16,
+                          const uint16_t* v16, float* out);
+/* Causal batch attention of M query rows at positions S..S+M-1 over cache
+ * rows [0, S+M) (the batch's own K/V already appended). */
+int mdx_debug_attn_prefill(int nq, int nkv, int hd, int S, int M, const float* q,
+                           const uint16_t* k16, const uint16_t* v16, float* out);
+/* QK-norm + RoPE + KV append of one token at position pos: qkv fp32
+ * [nq*hd + 2*nkv*hd]; returns q fp32 and the fp16 k,v rows. */
+int mdx_debug_qk_rope(int nq, int nkv, int hd, int pos, int rope_style, float theta, float eps,
+                      const float* q_norm, const float* k_norm, const float* qkv, float* q_out,
+                      uint16_t* k16, uint16_t* v16);
+/* Fused RMSNorm + lm_head + argmax on one hidden vector; lm_kind as
+ * mdx_debug_gemv's 1 (int8 rows [N,K] + scales), 3 or 4.  Returns the
+ * argmax and writes logits[N]. */
+int mdx_debug_lmhead(int lm_kind, int K, int N, const void* w_rows, const float* scales,
+                     const float* hidden, const float* norm_w, float eps, float* logits);
+
+/* ---- host helpers shared with tools (no GPU needed) ---- */
+
+/* INT8 lm_head quantiser of the reference (per vocab row of the fp16 copy):
+ * scale = max|v|/127, q = clamp((int)roundf(v * (127/max)), -128, 127). */
+void mdx_quantize_lm_head(int8_t* q, float* scales, const uint16_t* lm_f16, int V, int K);
+/* Round-to-nearest-even fp32 -> fp16 bits, and back. */
+uint16_t mdx_f32_to_f16(float f);
+float mdx_f16_to_f32(uint16_t h);
+/* SplitMix64 + Box-Muller N(mean, std) stream, in chunks of 2^20 values,
+ * seeded per tensor with mdx_synth_seed(base, name). */
+uint64_t mdx_synth_seed(uint64_t base, const char* name);
+void mdx_synth_fill_normal(float* out, size_t n, uint64_t seed, double mean, double std);
+
+/* Write a synthetic model directory in the reference on-disk format:
+ * config.json, embeddings.bin ~N(0, 0.02) fp32, layers/layer_LL/ with norm
+ * weights 1.0 and projections ~N(0, 0.02): quant 0 writes fp16 [K,N]
+ * <proj>.bin; quant 1 quantises per column (scale = max|col|/127) into
+ * <proj>_weight.bin int8 [K,N] + <proj>_scales.bin fp32; quant 2 writes
+ * int4 [K,N/2] (column 2j low nibble) with fp16-representable scales
+ * max|col|/7.  The lm_head is tied to the embeddings.  Returns 0. */
+int mdx_synth_write_model(const char* dir, const MatmulDecoderConfig* cfg, int quant,
+                          uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,108 @@
+// mdx_common.h — device helpers shared by the gfx950 kernels.
+//
+// Conversions follow round-to-nearest-even (the hardware default mode).
+// All code is compiled with -ffp-contract=off, so `a*b + c` rounds twice
+// unless a fused builtin is written explicitly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mdx {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Sum over all 64 lanes; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Sum over aligned groups of `width` lanes (power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// fp16 x fp16 products (exact in fp32) accumulated into fp32.
+__device__ __forceinline__ float dot8_f16(uint4 w, uint4 x, float acc) {
+    acc = __builtin_amdgcn_fdot2(as_h2(w.x), as_h2(x.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(as_h2(w.y), as_h2(x.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(as_h2(w.z), as_h2(x.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(as_h2(w.w), as_h2(x.w), acc, false);
+    return acc;
+}
+
+// Four signed int8 (one word, k ascending from the low byte) -> two half2
+// holding (q0,q1) and (q2,q3), exactly: (0x6400 | (q+128)) is 1024+q+128.
+__device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, half2_t& a, half2_t& b) {
+    const uint32_t u = w ^ 0x80808080u;
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    a = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+    b = as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+}
+
+// One int4 word of the device layout (8 consecutive k, nibble pairs
+// interleaved so that (w >> 4i) & 0x000f000f holds k=2i and k=2i+1) ->
+// half2 (q_{2i}, q_{2i+1}) exactly: (0x6400 | (q+8)) is 1024+q+8.
+__device__ __forceinline__ half2_t i4_pair(uint32_t u, int i) {
+    const half2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    return as_h2(((u >> (4 * i)) & 0x000f000fu) | 0x64006400u) - bias;
+}
+
+__device__ __forceinline__ float dot16_i8(uint4 w, uint4 x0, uint4 x1, float acc) {
+    half2_t a, b;
+    i8x4_to_h2x2(w.x, a, b);
+    acc = __builtin_amdgcn_fdot2(a, as_h2(x0.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(b, as_h2(x0.y), acc, false);
+    i8x4_to_h2x2(w.y, a, b);
+    acc = __builtin_amdgcn_fdot2(a, as_h2(x0.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(b, as_h2(x0.w), acc, false);
+    i8x4_to_h2x2(w.z, a, b);
+    acc = __builtin_amdgcn_fdot2(a, as_h2(x1.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(b, as_h2(x1.y), acc, false);
+    i8x4_to_h2x2(w.w, a, b);
+    acc = __builtin_amdgcn_fdot2(a, as_h2(x1.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(b, as_h2(x1.w), acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ float dot8_i4(uint32_t w, uint4 x, float acc) {
+    const uint32_t u = w ^ 0x88888888u;
+    acc = __builtin_amdgcn_fdot2(i4_pair(u, 0), as_h2(x.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(i4_pair(u, 1), as_h2(x.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(i4_pair(u, 2), as_h2(x.z), acc, false);
+    acc = __builtin_amdgcn_fdot2(i4_pair(u, 3), as_h2(x.w), acc, false);
+    return acc;
+}
+
+// Reference-style SiLU-gated product: g * (1 / (1 + expf(-g))) * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    float sig = 1.0f / (1.0f + expf(-g));
+    return (g * sig) * u;
+}
+
+}  // namespace mdx

@@ -1,0 +1,165 @@
+/*
+ * mdx_device.h — the thin C ABI between the host C runtime and the HIP
+ * kernels for gfx950.  Plain C types only: device pointers are `void*`,
+ * streams and graphs are opaque handles.  Every launcher returns 0 or a
+ * negative MatmulDecoderError code and never synchronises.
+ *
+ * Device weight layout (all projections): W^T, one row per output column
+ * n, K contiguous.  fp16 rows are K*2 bytes, int8 rows K bytes, int4 rows
+ * K/2 bytes made of 32-bit words of 8 consecutive k: bits [4i+3:4i] hold
+ * k=2i and bits [4i+19:4i+16] hold k=2i+1 (i = 0..3), two's complement
+ * [-8,7].  fp32 rows (multi-head lm_heads) are K*4 bytes.  Optional fp32
+ * per-row scales [N].
+ */
+#ifndef MDX_DEVICE_H
+#define MDX_DEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MDX_W_F16 = 0, MDX_W_I8 = 1, MDX_W_I4 = 2, MDX_W_F32 = 3 };
+
+/* One (possibly merged) projection resident in HBM. */
+typedef struct {
+    const void* w;          /* [N][K] in the layout above */
+    const float* scale;     /* [N] or NULL */
+    int kind;               /* MDX_W_* */
+    int K, N;
+} mdx_wdesc;
+
+/* Per-context decode state, resident in device memory. */
+typedef struct {
+    int pos;                /* position being written (KV rows [0,pos) are valid) */
+    int token;              /* input token when mode == 0; argmax output feeds it */
+    int mode;               /* 0 = gather embeddings[token], 1 = use the uploaded embedding */
+    int argmax;             /* last lm_head argmax */
+    int n_out;              /* tokens appended to the greedy output list */
+    int pad[3];
+} mdx_state;
+
+/* ---- runtime wrappers (mdx_rt.hip) ---- */
+int mdxrt_device_count(void);
+const char* mdxrt_last_error(void);
+int mdxrt_malloc(void** p, size_t bytes);
+int mdxrt_free(void* p);
+int mdxrt_host_alloc(void** p, size_t bytes);     /* pinned */
+int mdxrt_host_free(void* p);
+int mdxrt_h2d(void* dst, const void* src, size_t bytes);
+int mdxrt_d2h(void* dst, const void* src, size_t bytes);
+int mdxrt_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int mdxrt_d2h_async(void* dst, const void* src, size_t bytes, void* stream);
+int mdxrt_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
+int mdxrt_stream_create(void** stream);
+int mdxrt_stream_destroy(void* stream);
+int mdxrt_stream_sync(void* stream);
+int mdxrt_graph_begin(void* stream);
+int mdxrt_graph_end(void* stream, void** exec);
+int mdxrt_graph_launch(void* exec, void* stream);
+int mdxrt_graph_destroy(void* exec);
+int mdxrt_event_create(void** ev);
+int mdxrt_event_destroy(void* ev);
+int mdxrt_event_record(void* ev, void* stream);
+int mdxrt_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Fill `n` 32-bit words with `value` on the stream (a kernel, never a
+ * memset node, so it is safe inside captured graphs). */
+int mdxrt_fill_u32(void* dst, uint32_t value, size_t n, void* stream);
+
+/* ---- decode (M = 1) kernels ---- */
+
+/* hidden[d] fp32 <- embeddings[state->token] or emb_in, per state->mode. */
+int mdx_launch_embed(const mdx_state* state, const float* emb_table, const float* emb_in,
+                     float* hidden, int d, int vocab, void* stream);
+
+/* Fused RMSNorm + projection: x16 = fp16((hidden*rms)*norm_w), y = x16 . W^T
+ * (x scale).  epilogue: 0 store y fp32, 1 SwiGLU over rows [0,N/2) and
+ * [N/2,N) writing act fp16 [N/2]. */
+int mdx_launch_norm_gemv(const float* hidden, const float* norm_w, float eps,
+                         const mdx_wdesc* w, int epilogue, void* out, void* stream);
+
+/* y = fp16 x . W^T (x scale); out[n] += y[n] (residual add, fp32). */
+int mdx_launch_gemv_add(const uint16_t* x16, const mdx_wdesc* w, float* out, void* stream);
+
+/* y = x16 . W^T (x scale), fp16 input already rounded, fp32 output. */
+int mdx_launch_gemv_f16in(const uint16_t* x16, const mdx_wdesc* w, float* y, void* stream);
+
+/* Plain projection with fp32 output: y = x . W^T.  For MDX_W_F16/I8/I4 the
+ * fp32 x is rounded to fp16 (the NPU input); for MDX_W_F32 and when
+ * x_fp32_exact != 0 with MDX_W_F16 it is used as fp32 (the CPU GEMVs). */
+int mdx_launch_gemv(const float* x, const mdx_wdesc* w, int x_fp32_exact, float* y,
+                    void* stream);
+
+/* Per-head QK-norm + RoPE of q,k from the merged QKV output (fp32
+ * [q|k|v]); q written fp32 [nq*hd]; k,v appended as fp16 at row state->pos
+ * of the layer cache [max_seq][nkv*hd].  q_norm/k_norm may be NULL. */
+int mdx_launch_qk_rope_append(const mdx_state* state, const float* qkv, const float* q_norm,
+                              const float* k_norm, float eps, const float* cos_t,
+                              const float* sin_t, int nq, int nkv, int hd, int rope_style,
+                              float* q_out, uint16_t* k_cache, uint16_t* v_cache, void* stream);
+
+/* Split-K GQA decode attention over cache rows [0, state->pos]; writes the
+ * fp16 attention output [nq*hd].  part is scratch of
+ * mdx_attn_decode_scratch_floats(nq, hd, max_splits) floats; max_splits must
+ * be >= ceil(max_seq / 16). */
+size_t mdx_attn_decode_scratch_floats(int nq, int hd, int max_splits);
+int mdx_launch_attn_decode(const mdx_state* state, const float* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, int nq, int nkv, int hd, int max_seq,
+                           int max_splits, float* part, uint16_t* attn_out16, void* stream);
+
+/* Final RMSNorm + INT8 (or fp16/fp32-row) lm_head writing logits fp32 [N]
+ * and per-block (value,index) partials; then the argmax reduction.
+ * lm_kind: MDX_W_I8 (fp16 activations, the NPU path), MDX_W_F16 with fp32
+ * activations (the CPU fp16 GEMV), MDX_W_F32 (fp32 rows).
+ * partial holds mdx_lmhead_partials(N) pairs of 8 bytes. */
+int mdx_lmhead_partials(int N);
+int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
+                      float* logits, void* partial, void* stream);
+/* Reduces the partials to the argmax (lowest index on ties), stores it in
+ * state->argmax and state->token, appends it to out_tokens[state->n_out++]
+ * when out_tokens != NULL, and advances state->pos by `advance`. */
+int mdx_launch_argmax_finish(mdx_state* state, const void* partial, int n_partials,
+                             int* out_tokens, int advance, void* stream);
+/* state->pos += advance (prefill-mode steps). */
+int mdx_launch_advance(mdx_state* state, int advance, void* stream);
+
+/* ---- batch prefill (M <= 64) kernels ---- */
+
+/* x16[m][d] = fp16((x[m]*rms)*w) for m < M. */
+int mdx_launch_rmsnorm_rows(const float* x, const float* w, float eps, int M, int d,
+                            uint16_t* x16, void* stream);
+/* x16[m][k] = fp16(x[m][k]). */
+int mdx_launch_to_f16(const float* x, int n, uint16_t* x16, void* stream);
+
+/* Y = X16[M][K] . W^T on MFMA, M <= 64.  epilogue: 0 store fp32 y[M][N],
+ * 1 add into y[M][N], 2 SwiGLU (rows [0,N/2) gate, [N/2,N) up) -> fp16
+ * act[M][N/2].  scratch: mdx_gemm_scratch_floats(M, N, K) floats. */
+size_t mdx_gemm_scratch_floats(int M, int N, int K);
+int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
+                    float* scratch, void* stream);
+
+/* QK-norm + RoPE for rows t < M at positions start+t, appending k,v fp16
+ * at cache rows start+t; q written fp32 [M][nq*hd].  `start` is read from
+ * state->pos. */
+int mdx_launch_qk_rope_append_rows(const mdx_state* state, const float* qkv, int M,
+                                   const float* q_norm, const float* k_norm, float eps,
+                                   const float* cos_t, const float* sin_t, int nq, int nkv,
+                                   int hd, int rope_style, float* q_out, uint16_t* k_cache,
+                                   uint16_t* v_cache, void* stream);
+
+/* Causal attention for query rows t < M at positions state->pos + t over
+ * cache rows [0, state->pos + t]; output fp16 [M][nq*hd]. */
+int mdx_launch_attn_prefill(const mdx_state* state, const float* q, int M,
+                            const uint16_t* k_cache, const uint16_t* v_cache, int nq, int nkv,
+                            int hd, uint16_t* out16, void* stream);
+
+/* Copy row M-1 of x[M][d] to dst[d] (last-token hidden after prefill). */
+int mdx_launch_copy_row(const float* x, int row, int d, float* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

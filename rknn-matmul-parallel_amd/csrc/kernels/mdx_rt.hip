@@ -1,0 +1,175 @@
+// mdx_rt.hip — HIP runtime wrappers behind the plain-C device ABI
+// (mdx_device.h).  Errors are mapped to MatmulDecoderError codes and the
+// last HIP message is kept for diagnostics.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+
+#include "mdx_device.h"
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+int fail(hipError_t e, const char* what) {
+    std::snprintf(g_last_error, sizeof g_last_error, "%s: %s", what, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? -2 : -4;
+}
+
+#define MDX_CHECK(expr, what)                     \
+    do {                                          \
+        hipError_t e_ = (expr);                   \
+        if (e_ != hipSuccess) return fail(e_, what); \
+    } while (0)
+
+__global__ void k_fill_u32(uint32_t* dst, uint32_t value, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = value;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdxrt_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+const char* mdxrt_last_error(void) { return g_last_error; }
+
+int mdxrt_malloc(void** p, size_t bytes) {
+    *p = nullptr;
+    MDX_CHECK(hipMalloc(p, bytes ? bytes : 256), "hipMalloc");
+    return 0;
+}
+
+int mdxrt_free(void* p) {
+    if (p) MDX_CHECK(hipFree(p), "hipFree");
+    return 0;
+}
+
+int mdxrt_host_alloc(void** p, size_t bytes) {
+    *p = nullptr;
+    MDX_CHECK(hipHostMalloc(p, bytes ? bytes : 64, hipHostMallocDefault), "hipHostMalloc");
+    return 0;
+}
+
+int mdxrt_host_free(void* p) {
+    if (p) MDX_CHECK(hipHostFree(p), "hipHostFree");
+    return 0;
+}
+
+int mdxrt_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes) MDX_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+    return 0;
+}
+
+int mdxrt_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes) MDX_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return 0;
+}
+
+int mdxrt_h2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes)
+        MDX_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream),
+                  "hipMemcpyAsync H2D");
+    return 0;
+}
+
+int mdxrt_d2h_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes)
+        MDX_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream),
+                  "hipMemcpyAsync D2H");
+    return 0;
+}
+
+int mdxrt_d2d_async(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes)
+        MDX_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                  "hipMemcpyAsync D2D");
+    return 0;
+}
+
+int mdxrt_stream_create(void** stream) {
+    hipStream_t s = nullptr;
+    MDX_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *stream = (void*)s;
+    return 0;
+}
+
+int mdxrt_stream_destroy(void* stream) {
+    if (stream) MDX_CHECK(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy");
+    return 0;
+}
+
+int mdxrt_stream_sync(void* stream) {
+    MDX_CHECK(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    return 0;
+}
+
+int mdxrt_graph_begin(void* stream) {
+    MDX_CHECK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
+              "hipStreamBeginCapture");
+    return 0;
+}
+
+int mdxrt_graph_end(void* stream, void** exec) {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    *exec = nullptr;
+    MDX_CHECK(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(e, "hipGraphInstantiate");
+    *exec = (void*)ge;
+    return 0;
+}
+
+int mdxrt_graph_launch(void* exec, void* stream) {
+    MDX_CHECK(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream), "hipGraphLaunch");
+    return 0;
+}
+
+int mdxrt_graph_destroy(void* exec) {
+    if (exec) MDX_CHECK(hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+    return 0;
+}
+
+int mdxrt_event_create(void** ev) {
+    hipEvent_t e = nullptr;
+    MDX_CHECK(hipEventCreate(&e), "hipEventCreate");
+    *ev = (void*)e;
+    return 0;
+}
+
+int mdxrt_event_destroy(void* ev) {
+    if (ev) MDX_CHECK(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy");
+    return 0;
+}
+
+int mdxrt_event_record(void* ev, void* stream) {
+    MDX_CHECK(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream), "hipEventRecord");
+    return 0;
+}
+
+int mdxrt_event_elapsed_ms(void* start, void* stop, float* ms) {
+    MDX_CHECK(hipEventSynchronize((hipEvent_t)stop), "hipEventSynchronize");
+    MDX_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop), "hipEventElapsedTime");
+    return 0;
+}
+
+int mdxrt_fill_u32(void* dst, uint32_t value, size_t n, void* stream) {
+    if (!n) return 0;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    k_fill_u32<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+        (uint32_t*)dst, value, n);
+    MDX_CHECK(hipGetLastError(), "k_fill_u32");
+    return 0;
+}
+
+}  // extern "C"

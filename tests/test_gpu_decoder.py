@@ -1,0 +1,283 @@
+"""End-to-end GPU parity of the decoder C ABI (matmul_decoder.h) against the
+oracle decoder on tiny seeded models in the reference on-disk format: logits
+per step (rel <= 1e-3, cosine >= 0.9999), greedy tokens identical, batch
+prefill, multi-head step_head, the fp16 CPU-style lm_head, error returns,
+graph replays, the device greedy loop, the pybind module and rmp_*."""
+import ctypes
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import PKG, cosine, rel_err, tiny_config
+
+pytestmark = pytest.mark.gpu
+
+QNAME = {0: "fp16", 1: "int8", 2: "int4"}
+
+
+@pytest.fixture(scope="module")
+def models(mdx, workdir):
+    out = {}
+    for quant in (0, 1, 2):
+        cfg, d = tiny_config(mdx)
+        path = os.path.join(workdir, f"gpu_tiny_{quant}")
+        mdx.write_model(path, cfg, quant, 4242 + quant)
+        out[quant] = (path, cfg, d)
+    return out
+
+
+def _pair(mdx, oracle_lib, models, quant, max_seq=96, **over):
+    path, cfg, d = models[quant]
+    if over:
+        cfg, d = tiny_config(mdx, **over)
+    g = mdx.Decoder(path, cfg, QNAME[quant], max_seq)
+    o = oracle_lib.Model(path, d, quant, max_seq, kv_fp16=True)
+    return g, o, d
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_greedy_steps_match_oracle(mdx, gpu, oracle_lib, models, quant):
+    g, o, d = _pair(mdx, oracle_lib, models, quant)
+    tok_g = tok_o = 151 % d["vocab_size"]
+    for step in range(16):
+        tok_g, lg = g.step(tok_g)
+        tok_o, lo = o.step(tok_o)
+        assert rel_err(lg, lo) < 1e-3 and cosine(lg, lo) > 0.9999, f"step {step}"
+        assert tok_g == tok_o, f"step {step}"
+    assert g.seq_len == o.seq_len == 16
+    st = g.stats()
+    assert st["n_steps"] == 16 and st["total_ms"] > 0 and st["rebind_ms"] == 0
+
+
+@pytest.mark.parametrize("quant", [0, 1])
+def test_batch_prefill_then_decode(mdx, gpu, oracle_lib, models, quant):
+    g, o, d = _pair(mdx, oracle_lib, models, quant)
+    emb = np.random.default_rng(9).standard_normal((23, d["hidden_dim"])).astype(np.float32)
+    assert g.prefill_batch(emb) == 0 and o.prefill_batch(emb) == 0
+    for layer in range(d["num_layers"]):
+        kg, vg = g.kv_read(layer, 0, 23)
+        ko, vo = o.kv_read(layer, 0, 23)
+        assert rel_err(kg, ko) < 2e-3 and rel_err(vg, vo) < 2e-3
+    for t in (3, 99, 200):
+        tg, lg = g.step(t)
+        to, lo = o.step(t)
+        assert tg == to and rel_err(lg, lo) < 1e-3
+
+
+def test_prefill_longer_than_one_chunk(mdx, gpu, oracle_lib, models):
+    g, o, d = _pair(mdx, oracle_lib, models, 0, max_seq=128)
+    emb = np.random.default_rng(10).standard_normal((70, d["hidden_dim"])).astype(np.float32)
+    assert g.prefill_batch(emb) == 0 and o.prefill_batch(emb) == 0
+    assert g.seq_len == 70
+    tg, lg = g.step(5)
+    to, lo = o.step(5)
+    assert tg == to and rel_err(lg, lo) < 1e-3
+
+
+def test_prefill_logits_last_token(mdx, gpu, oracle_lib, models):
+    g, o, d = _pair(mdx, oracle_lib, models, 1)
+    emb = np.random.default_rng(11).standard_normal((60, d["hidden_dim"])).astype(np.float32)
+    tok, lg = g.prefill_logits(emb)
+    assert o.prefill_batch(emb) == 0
+    x16 = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(o.last_normed())).astype(np.float64)
+    q, s = o.lm_head_q()
+    ref = (q.astype(np.float64) @ x16) * s
+    assert cosine(lg, ref) > 0.9999 and rel_err(lg, ref) < 1e-3 and tok == int(np.argmax(ref))
+    assert g.seq_len == 60
+
+
+def test_embedding_input_and_prefill_mode(mdx, gpu, oracle_lib, models):
+    g, o, d = _pair(mdx, oracle_lib, models, 0)
+    rng = np.random.default_rng(12)
+    for _ in range(5):
+        e = rng.standard_normal(d["hidden_dim"]).astype(np.float32)
+        assert g.step(0, e, logits=False)[0] == 0
+        assert o.step(0, e, logits=False)[0] == 0
+    e = rng.standard_normal(d["hidden_dim"]).astype(np.float32)
+    tg, lg = g.step(0, e)
+    to, lo = o.step(0, e)
+    assert tg == to and rel_err(lg, lo) < 1e-3
+    assert g.step_token(tg) == o.step(to)[0]
+
+
+def test_cpu_style_fp16_lm_head(mdx, gpu, oracle_lib, models):
+    g, o, d = _pair(mdx, oracle_lib, models, 0, disable_npu_lm_head=1)
+    for t in (1, 2, 3):
+        tg, lg = g.step(t)
+        to, lo = o.step(t)
+        assert tg == to and rel_err(lg, lo) < 1e-3
+
+
+def test_multi_head_step_head(mdx, gpu, oracle_lib, workdir):
+    cfg, d = tiny_config(mdx, num_lm_heads=3, lm_head_vocab_size=200, tie_word_embeddings=0)
+    path = os.path.join(workdir, "gpu_multihead")
+    mdx.write_model(path, cfg, 0, 77)
+    g = mdx.Decoder(path, cfg, "fp16", 32)
+    o = oracle_lib.Model(path, d, 0, 32)
+    for i, head in enumerate((0, 2, 1, 2)):
+        tg, lg = g.step_head(10 + i, head)
+        to, lo = o.step_head(10 + i, head, n_logits=200)
+        assert tg == to and rel_err(lg, lo) < 1e-3
+    assert g.step_head(1, 3)[0] == -1 and g.step_head(1, -1)[0] == -1
+
+
+def test_error_returns(mdx, gpu, models):
+    path, cfg, d = models[0]
+    g = mdx.Decoder(path, cfg, "fp16", 4)
+    assert g.step(-1)[0] == -1 and g.step(d["vocab_size"])[0] == -1
+    for _ in range(4):
+        assert g.step(1, logits=False)[0] == 0
+    assert g.step(1)[0] == -1 and g.seq_len == 4
+    g.clear()
+    assert g.seq_len == 0
+    assert g.prefill_batch(np.zeros((5, d["hidden_dim"]), np.float32)) == -1
+    assert g.step(2)[0] >= 0
+
+
+def test_replays_are_deterministic(mdx, gpu, models):
+    path, cfg, d = models[1]
+    g = mdx.Decoder(path, cfg, "int8", 64)
+    runs = []
+    for _ in range(3):
+        g.clear()
+        seq = [g.step(t)[1] for t in (5, 6, 7, 8)]
+        runs.append(np.stack(seq))
+    assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[0], runs[2])
+
+
+def test_device_greedy_loop_equals_steps(mdx, gpu, models):
+    path, cfg, d = models[0]
+    g = mdx.Decoder(path, cfg, "fp16", 96)
+    toks, ms = g.generate_greedy(42, 20)
+    assert ms > 0 and g.seq_len == 20
+    g.clear()
+    t, want = 42, []
+    for _ in range(20):
+        t, _ = g.step(t)
+        want.append(t)
+    assert toks == want
+
+
+def test_kv_fill_hook_matches_oracle(mdx, gpu, oracle_lib, models):
+    g, o, d = _pair(mdx, oracle_lib, models, 0)
+    g.kv_fill_normal(50, 123)
+    assert o.kv_fill_normal(50, 123) == 0 and g.seq_len == 50
+    for layer in range(d["num_layers"]):
+        kg, vg = g.kv_read(layer, 0, 50)
+        ko, vo = o.kv_read(layer, 0, 50)
+        assert np.array_equal(kg, ko) and np.array_equal(vg, vo)
+    tg, lg = g.step(17)
+    to, lo = o.step(17)
+    assert tg == to and rel_err(lg, lo) < 1e-3
+
+
+def test_create_from_weights_equals_model_dir(mdx, gpu, models):
+    path, cfg, d = models[1]
+    L = mdx.lib()
+    K = {"q": (d["hidden_dim"], 256), "k": (d["hidden_dim"], 128), "v": (d["hidden_dim"], 128),
+         "o": (256, d["hidden_dim"]), "gate": (d["hidden_dim"], d["ffn_dim"]),
+         "up": (d["hidden_dim"], d["ffn_dim"]), "down": (d["ffn_dim"], d["hidden_dim"])}
+    keep = []
+
+    class PW(ctypes.Structure):
+        _fields_ = [("data", ctypes.c_void_p), ("scales", ctypes.POINTER(ctypes.c_float)),
+                    ("K", ctypes.c_int), ("N", ctypes.c_int), ("quant_type", ctypes.c_int)]
+
+    class LW(ctypes.Structure):
+        _fields_ = [(n, PW) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                      "down_proj")] + [(n, ctypes.POINTER(ctypes.c_float)) for n in (
+                                          "input_norm_weight", "post_attn_norm_weight",
+                                          "q_norm_weight", "k_norm_weight")]
+
+    def f32(p):
+        a = np.fromfile(p, np.float32)
+        keep.append(a)
+        return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+    layers = (LW * d["num_layers"])()
+    for l in range(d["num_layers"]):
+        ld = os.path.join(path, "layers", f"layer_{l:02d}")
+        for n, (k_, n_) in K.items():
+            w = np.fromfile(os.path.join(ld, f"{n}_proj_weight.bin"), np.int8)
+            keep.append(w)
+            setattr(layers[l], f"{n}_proj", PW(w.ctypes.data, f32(os.path.join(ld, f"{n}_proj_scales.bin")),
+                                              k_, n_, 1))
+        layers[l].input_norm_weight = f32(os.path.join(ld, "input_norm.bin"))
+        layers[l].post_attn_norm_weight = f32(os.path.join(ld, "post_attn_norm.bin"))
+        layers[l].q_norm_weight = f32(os.path.join(ld, "q_norm.bin"))
+        layers[l].k_norm_weight = f32(os.path.join(ld, "k_norm.bin"))
+    emb = np.fromfile(os.path.join(path, "embeddings.bin"), np.float32)
+    L.matmul_decoder_create_from_weights.restype = ctypes.c_void_p
+    L.matmul_decoder_create_from_weights.argtypes = [ctypes.POINTER(mdx.MatmulDecoderConfig),
+                                                     ctypes.c_void_p, ctypes.c_void_p,
+                                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    h = L.matmul_decoder_create_from_weights(ctypes.byref(cfg), emb.ctypes.data,
+                                             ctypes.addressof(layers), None, 1, 32)
+    assert h
+    try:
+        a = mdx.Decoder(path, cfg, "int8", 32)
+        la = np.empty(d["vocab_size"], np.float32)
+        ta = L.matmul_decoder_step(h, 9, None, la.ctypes.data_as(mdx._F))
+        tb, lb = a.step(9)
+        assert ta == tb and np.array_equal(la, lb)
+    finally:
+        L.matmul_decoder_destroy(h)
+
+
+def test_pybind_module_end_to_end(mdx, gpu, oracle_lib, models):
+    sys.path.insert(0, PKG)
+    import matmul_decoder as md
+    path, cfg, d = models[0]
+    dec = md.MatmulDecoder(path, max_seq_len=64, quant_type="fp16", exec_mode="single_core")
+    assert dec.config["hidden_dim"] == d["hidden_dim"] and dec.config["exec_mode"] == "single_core"
+    o = oracle_lib.Model(path, {**d, "rope_style": 1}, 0, 64)
+    rng = np.random.default_rng(13)
+    emb = rng.standard_normal((4, d["hidden_dim"])).astype(np.float32)
+    dec.prefill(0, emb)                       # 2-D routes to prefill_batch
+    assert o.prefill_batch(emb) == 0 and dec.seq_len == 4
+    dec.prefill(0, emb[0])                    # prefill mode step
+    o.step(0, emb[0], logits=False)
+    lg = dec.step(7)
+    to, lo = o.step(7)
+    assert int(np.argmax(lg)) == to and rel_err(lg, lo) < 1e-3
+    t = dec.step_get_token(to)
+    assert t == o.step(to)[0]
+    s = dec.stats
+    assert s["n_steps"] >= 3 and "lm_head_ms" in s
+    dec.clear_kv_cache()
+    out = dec.generate([3, 4, 5], max_new_tokens=6)
+    o2 = oracle_lib.Model(path, d, 0, 64)
+    o2.step(3, logits=False)
+    o2.step(4, logits=False)
+    want, t = [], 5
+    for _ in range(6):
+        t, _ = o2.step(t)
+        want.append(t)
+    assert out == want
+    with pytest.raises(RuntimeError):
+        dec.prefill_batch(np.zeros((100, d["hidden_dim"]), np.float32))
+
+
+@pytest.mark.parametrize("M", [1, 5, 64, 70])
+def test_rmp_run_matches_oracle(mdx, gpu, oracle_lib, M):
+    L = mdx.lib()
+    K, N = 1024, 1024
+    rng = np.random.default_rng(M)
+    w = (rng.standard_normal((K, N)) * 0.05).astype(np.float16)
+    cfg = mdx.RmpConfig(M=M, K=K, N=N, type=0, layout=0, n_workers=2)
+    h = L.rmp_create(ctypes.byref(cfg), w.ctypes.data, None)
+    assert h
+    try:
+        x = rng.standard_normal((M, K)).astype(np.float16)
+        y = np.empty((M, N), np.float32)
+        assert L.rmp_run(h, x.view(np.uint16).ctypes.data_as(mdx._U16), y.ctypes.data_as(mdx._F)) == 0
+        ref = oracle_lib.matmul(0, x.astype(np.float32), w.view(np.uint16), None, M, K, N)
+        assert rel_err(y, ref) < 1e-4
+        ms = L.rmp_benchmark(h, 5)
+        assert ms > 0 and abs(L.rmp_get_single_core_time(h) - ms * 1.37) < 1e-3 * ms + 1e-6
+    finally:
+        L.rmp_destroy(h)
+    bad = mdx.RmpConfig(M=1, K=1024, N=1023, type=0, layout=0, n_workers=2)
+    assert not L.rmp_create(ctypes.byref(bad), w.ctypes.data, None)

@@ -1,0 +1,223 @@
+"""GPU parity of each hand-written kernel against the oracle, through the C ABI
+single-kernel entry points (mdx_ext.h).  Bars: INT8 dot products bit-exact on
+integer-valued known-answer inputs; floating point within 1e-3 of the
+oracle measured as max|gpu - oracle| / max|oracle| ("rel"), with the
+tolerance written at each check."""
+import numpy as np
+import pytest
+
+from conftest import cosine, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3          # north-star bound per projection
+
+
+def _f16_bits(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def _pack_i4(q):
+    u = (q & 0xF).astype(np.uint8)
+    return (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+
+
+# ---- M = 1 projections -------------------------------------------------------------
+
+LAYER_SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024)]
+
+
+@pytest.mark.parametrize("K,N", LAYER_SHAPES)
+def test_gemv_fp16_layer_projection(mdx, gpu, oracle_lib, K, N):
+    rng = np.random.default_rng(K * 7 + N)
+    x = rng.standard_normal(K).astype(np.float32)
+    w = _f16_bits(rng.standard_normal((K, N)) * 0.02)
+    y = mdx.gemv(0, K, N, w, None, x)
+    ref = oracle_lib.matmul(0, x, w, None, 1, K, N)[0]
+    assert rel_err(y, ref) < TOL * 0.1
+
+
+def test_gemv_int8_lm_head_tile(mdx, gpu, oracle_lib):
+    """1 x 1024 x 4096 INT8 tile: int8 U[-127,127], fp32 scales U[1e-3,1e-2], x ~N(0,1)."""
+    rng = np.random.default_rng(1001)
+    K, N = 1024, 4096
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = mdx.gemv(1, K, N, q, s, x)
+    ref = oracle_lib.matmul(1, x, q, s, 1, K, N)[0]
+    assert rel_err(y, ref) < TOL * 0.1
+
+
+@pytest.mark.parametrize("K,N", [(1024, 4096), (3072, 1024), (2048, 96)])
+def test_gemv_int8_known_answer_bit_exact(mdx, gpu, oracle_lib, K, N):
+    rng = np.random.default_rng(K + 3 * N)
+    x = rng.integers(-16, 17, K).astype(np.float32)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    exact = (x.astype(np.int64) @ q.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(mdx.gemv(1, K, N, q, None, x), exact)
+    s = np.ones(N, np.float32)
+    assert np.array_equal(mdx.gemv(1, K, N, q, s, x), exact)
+
+
+def test_gemv_int4_all_codes_and_random(mdx, gpu, oracle_lib):
+    K, N = 1024, 256
+    q = ((np.arange(K)[:, None] * 5 + np.arange(N)[None, :]) % 16 - 8).astype(np.int64)
+    packed = _pack_i4(q)
+    s = np.linspace(0.25, 2.0, N).astype(np.float32)
+    for k in (0, 1, 7, 8, 31, 1023):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        assert np.array_equal(mdx.gemv(2, K, N, packed, s, x), q[k].astype(np.float32) * s)
+    rng = np.random.default_rng(5)
+    xi = rng.integers(-16, 17, K).astype(np.float32)
+    assert np.array_equal(mdx.gemv(2, K, N, packed, None, xi),
+                          (xi.astype(np.int64) @ q).astype(np.float32))
+    for K2, N2 in ((1024, 2048), (3072, 1024)):
+        qr = rng.integers(-8, 8, (K2, N2))
+        sr = _f16_bits(rng.uniform(1e-3, 3e-3, N2)).view(np.float16).astype(np.float32)
+        x = rng.standard_normal(K2).astype(np.float32)
+        y = mdx.gemv(2, K2, N2, _pack_i4(qr), sr, x)
+        ref = oracle_lib.matmul(2, x, _pack_i4(qr), sr, 1, K2, N2)[0]
+        assert rel_err(y, ref) < TOL * 0.1
+
+
+def test_gemv_fp32_activation_rows(mdx, gpu, oracle_lib):
+    rng = np.random.default_rng(6)
+    K, N = 1024, 2048
+    x = rng.standard_normal(K).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    assert rel_err(mdx.gemv(3, K, N, w, None, x), oracle_lib.gemv_rows_f32(x, w, N, K)) < 1e-5
+    w16 = _f16_bits(w)
+    assert rel_err(mdx.gemv(4, K, N, w16, None, x), oracle_lib.gemv_rows_f16(x, w16, N, K)) < 1e-5
+
+
+# ---- M <= 64 MFMA projections ------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("M,K,N", [(60, 1024, 4096), (60, 3072, 1024), (1, 1024, 1024),
+                                   (64, 2048, 1024), (7, 1024, 6144)])
+def test_gemm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
+    rng = np.random.default_rng(M * 31 + K + N + kind)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if kind == 0:
+        w, s = _f16_bits(rng.standard_normal((K, N)) * 0.02), None
+    elif kind == 1:
+        w, s = rng.integers(-127, 128, (K, N)).astype(np.int8), rng.uniform(1e-4, 2e-4, N).astype(np.float32)
+    else:
+        w, s = _pack_i4(rng.integers(-8, 8, (K, N))), rng.uniform(1e-3, 3e-3, N).astype(np.float32)
+    y = mdx.gemm(kind, M, K, N, w, s, x)
+    ref = oracle_lib.matmul(kind, x, w, s, M, K, N)
+    assert rel_err(y, ref) < TOL * 0.1
+
+
+def test_gemm_int8_known_answer_bit_exact(mdx, gpu):
+    rng = np.random.default_rng(77)
+    M, K, N = 60, 3072, 256
+    x = rng.integers(-16, 17, (M, K)).astype(np.float32)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    exact = (x.astype(np.int64) @ q.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(mdx.gemm(1, M, K, N, q, None, x), exact)
+
+
+# ---- attention -----------------------------------------------------------------------
+
+def _kv(rng, L, kvd):
+    k = rng.standard_normal(L * kvd).astype(np.float16)
+    v = rng.standard_normal(L * kvd).astype(np.float16)
+    return k, v
+
+
+@pytest.mark.parametrize("L", [1, 2, 17, 513, 576, 4097])
+def test_attention_decode(mdx, gpu, oracle_lib, L):
+    rng = np.random.default_rng(L)
+    nq, nkv, hd = 16, 8, 128
+    q = rng.standard_normal(nq * hd).astype(np.float32)
+    k, v = _kv(rng, L, nkv * hd)
+    out = mdx.attn_decode(nq, nkv, hd, L, q, k.view(np.uint16), v.view(np.uint16))
+    ref = oracle_lib.attention(q, k.astype(np.float32), v.astype(np.float32), nq, nkv, hd, L)
+    ref16 = ref.astype(np.float16).astype(np.float32)
+    assert rel_err(out, ref16) < TOL
+    if L == 1:
+        assert np.array_equal(out, np.repeat(v.astype(np.float32).reshape(nkv, hd), 2, axis=0).ravel())
+
+
+@pytest.mark.parametrize("S,M", [(0, 60), (0, 1), (100, 33), (4000, 64)])
+def test_attention_prefill(mdx, gpu, oracle_lib, S, M):
+    rng = np.random.default_rng(S + M)
+    nq, nkv, hd = 16, 8, 128
+    kvd = nkv * hd
+    q = rng.standard_normal(M * nq * hd).astype(np.float32)
+    k, v = _kv(rng, S + M, kvd)
+    out = mdx.attn_prefill(nq, nkv, hd, S, M, q, k.view(np.uint16), v.view(np.uint16))
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    ref = oracle_lib.attention_batch_causal(q, kf[S * kvd:], vf[S * kvd:], kf[:S * kvd], vf[:S * kvd],
+                                            M, nq, nkv, hd, S).reshape(M, -1)
+    assert rel_err(out, ref.astype(np.float16).astype(np.float32)) < TOL
+
+
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("pos", [0, 1, 4000])
+def test_qk_norm_rope_append(mdx, gpu, oracle_lib, style, pos):
+    rng = np.random.default_rng(pos * 2 + style)
+    nq, nkv, hd = 16, 8, 128
+    qkv = rng.standard_normal(nq * hd + 2 * nkv * hd).astype(np.float32) * 2
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    q, k16, v16 = mdx.qk_rope(nq, nkv, hd, pos, style, 1e6, 1e-6, qn, kn, qkv)
+    c, s = oracle_lib.rope_tables(pos + 1, hd, 1e6)
+    qd = nq * hd
+    qref = np.concatenate([oracle_lib.rms_norm(qkv[h * hd:(h + 1) * hd], qn, 1e-6) for h in range(nq)])
+    kref = np.concatenate([oracle_lib.rms_norm(qkv[qd + h * hd:qd + (h + 1) * hd], kn, 1e-6)
+                           for h in range(nkv)])
+    qref = oracle_lib.apply_rope(qref, c[pos], s[pos], nq, hd, style)
+    kref = oracle_lib.apply_rope(kref, c[pos], s[pos], nkv, hd, style)
+    assert rel_err(q, qref) < 1e-5
+    k = k16.view(np.float16).astype(np.float32)
+    assert rel_err(k, kref.astype(np.float16).astype(np.float32)) < 1e-3
+    assert np.array_equal(v16, qkv[qd + nkv * hd:].astype(np.float16).view(np.uint16))
+
+
+# ---- lm_head + argmax ------------------------------------------------------------------
+
+@pytest.mark.parametrize("V", [151936, 5000])
+def test_lm_head_int8_argmax(mdx, gpu, oracle_lib, V):
+    rng = np.random.default_rng(V)
+    K = 1024
+    lm = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    q, s = oracle_lib.quantize_lm_head(oracle_lib.f32_to_f16(lm), V, K)
+    h = rng.standard_normal(K).astype(np.float32)
+    nw = np.ones(K, np.float32)
+    tok, lg = mdx.lmhead(1, K, V, q, s, h, nw, 1e-6)
+    x16 = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(oracle_lib.rms_norm(h, nw, 1e-6)))
+    ref = (q.astype(np.float64) @ x16.astype(np.float64)) * s
+    assert rel_err(lg, ref) < TOL * 0.1 and cosine(lg, ref) > 0.9999
+    assert tok == int(np.argmax(lg))
+    top2 = np.sort(ref)[-2:]
+    if top2[1] - top2[0] > 1e-4 * np.abs(ref).max():
+        assert tok == int(np.argmax(ref))
+
+
+def test_lm_head_argmax_ties_pick_lowest_index(mdx, gpu):
+    K, V = 64, 4096
+    q = np.zeros((V, K), np.int8)
+    q[[10, 700, 3000], 0] = 5                       # three equal maxima
+    s = np.ones(V, np.float32)
+    h = np.zeros(K, np.float32)
+    h[0] = 1.0
+    tok, lg = mdx.lmhead(1, K, V, q, s, h, np.ones(K, np.float32), 1e-6)
+    assert tok == 10 and lg[10] == lg[700] == lg[3000]
+
+
+def test_lm_head_fp32_and_fp16_rows(mdx, gpu, oracle_lib):
+    rng = np.random.default_rng(11)
+    K, V = 1024, 2048
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    h = rng.standard_normal(K).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    x = oracle_lib.rms_norm(h, nw, 1e-6)
+    tok, lg = mdx.lmhead(3, K, V, w, None, h, nw, 1e-6)
+    assert rel_err(lg, oracle_lib.gemv_rows_f32(x, w, V, K)) < 1e-5 and tok == int(np.argmax(lg))
+    w16 = _f16_bits(w)
+    tok, lg = mdx.lmhead(4, K, V, w16, None, h, nw, 1e-6)
+    assert rel_err(lg, oracle_lib.gemv_rows_f16(x, w16, V, K)) < 1e-5 and tok == int(np.argmax(lg))
