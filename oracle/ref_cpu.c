@@ -48,21 +48,31 @@ uint16_t orc_f32_to_f16(float f) {
     }
 }
 
-/* Exact widening (reference: src/cpu_ops.c:396-406). Subnormal halves are
- * rescaled by 2^112, which is exact. */
-float orc_f16_to_f32(uint16_t h) {
-    uint32_t a = (uint32_t)(h & 0x7fffu) << 13;
-    float f = u2f(a) * 0x1p112f;
-    if ((h & 0x7c00u) == 0x7c00u) f = u2f(a | 0x7f800000u);
-    return (h & 0x8000u) ? -f : f;
+/* Exact widening (reference: src/cpu_ops.c:396-406).  Normal halves rebias
+ * the exponent, subnormal halves are mantissa * 2^-24 (exact, and never a
+ * denormal fp32 operand), inf/NaN keep their payload; integer masks select
+ * the case so that loops over it vectorise. */
+static inline float f16_widen(uint16_t h) {
+    const uint32_t e = h & 0x7c00u;
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t normal = ((uint32_t)(h & 0x7fffu) << 13) + (112u << 23);
+    const uint32_t sub = f2u((float)(int32_t)(h & 0x3ffu) * 0x1p-24f);
+    const uint32_t special = ((uint32_t)(h & 0x3ffu) << 13) | 0x7f800000u;
+    const uint32_t is_sub = 0u - (uint32_t)(e == 0);
+    const uint32_t is_spec = 0u - (uint32_t)(e == 0x7c00u);
+    uint32_t r = (normal & ~is_sub) | (sub & is_sub);
+    r = (r & ~is_spec) | (special & is_spec);
+    return u2f(r | sign);
 }
+
+float orc_f16_to_f32(uint16_t h) { return f16_widen(h); }
 
 void orc_vec_f32_to_f16(uint16_t* dst, const float* src, size_t n) {
     for (size_t i = 0; i < n; i++) dst[i] = orc_f32_to_f16(src[i]);
 }
 
 void orc_vec_f16_to_f32(float* dst, const uint16_t* src, size_t n) {
-    for (size_t i = 0; i < n; i++) dst[i] = orc_f16_to_f32(src[i]);
+    for (size_t i = 0; i < n; i++) dst[i] = f16_widen(src[i]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -316,7 +326,7 @@ void orc_matmul_f16(float* y, const float* x, const uint16_t* w, int M, int K, i
     }
     for (int k = 0; k < K; k++) {
         const uint16_t* wk = w + (size_t)k * N;
-        for (int n = 0; n < N; n++) wrow[n] = orc_f16_to_f32(wk[n]);
+        for (int n = 0; n < N; n++) wrow[n] = f16_widen(wk[n]);
         for (int m = 0; m < M; m++) {
             float xk = orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k]));
             float* ym = y + (size_t)m * N;
@@ -352,9 +362,10 @@ void orc_matmul_i4(float* y, const float* x, const uint8_t* q, const float* scal
     for (size_t i = 0; i < (size_t)M * N; i++) y[i] = 0.0f;
     for (int k = 0; k < K; k++) {
         const uint8_t* qk = q + (size_t)k * (N / 2);
-        for (int n = 0; n < N; n++) {
-            int nib = (n & 1) ? (qk[n >> 1] >> 4) : (qk[n >> 1] & 0xf);
-            wrow[n] = (float)(nib >= 8 ? nib - 16 : nib);
+        for (int j = 0; j < N / 2; j++) {
+            /* sign-extend each nibble: column 2j low, 2j+1 high */
+            wrow[2 * j] = (float)((int8_t)(uint8_t)(qk[j] << 4) >> 4);
+            wrow[2 * j + 1] = (float)((int8_t)qk[j] >> 4);
         }
         for (int m = 0; m < M; m++) {
             float xk = orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k]));
@@ -440,7 +451,8 @@ struct orc_model {
     float* emb;
     float* lm_f32;           /* single head, fp32 (may alias emb) */
     uint16_t* lm_f16;
-    int8_t* lm_q;
+    int8_t* lm_q;            /* [V][K] as quantised */
+    int8_t* lm_qt;           /* [K][V]: the NPU B-matrix orientation */
     float* lm_s;
     float** lm_heads;        /* multi-head */
     orc_layer* layers;
@@ -554,6 +566,10 @@ orc_model* orc_model_open(const char* dir, const orc_config* c, int quant, int m
             m->lm_q = (int8_t*)malloc((size_t)V * d);
             m->lm_s = (float*)malloc((size_t)V * 4);
             orc_quantize_lm_head(m->lm_q, m->lm_s, m->lm_f16, V, d);
+            m->lm_qt = (int8_t*)malloc((size_t)V * d);
+            if (!m->lm_qt) goto fail;
+            for (int v = 0; v < V; v++)
+                for (int k = 0; k < d; k++) m->lm_qt[(size_t)k * V + v] = m->lm_q[(size_t)v * d + k];
         }
     }
     m->layers = (orc_layer*)calloc((size_t)c->num_layers, sizeof(orc_layer));
@@ -612,7 +628,7 @@ void orc_model_close(orc_model* m) {
         free(m->lm_heads);
     }
     if (m->lm_f32 != m->emb) free(m->lm_f32);
-    free(m->emb); free(m->lm_f16); free(m->lm_q); free(m->lm_s);
+    free(m->emb); free(m->lm_f16); free(m->lm_q); free(m->lm_qt); free(m->lm_s);
     free(m->kc); free(m->vc); free(m->cos_t); free(m->sin_t);
     free(m->hidden); free(m->residual); free(m->normed); free(m->q); free(m->k); free(m->v);
     free(m->attn); free(m->gate); free(m->up); free(m->down); free(m->logits);
@@ -683,16 +699,9 @@ int orc_model_step(orc_model* m, int token_id, const float* embedding, float* lo
     int d = c->hidden_dim, V = c->vocab_size;
     orc_rms_norm(m->normed, m->hidden, m->final_norm, d, c->rms_eps);
     if (m->lm_q) {
-        /* logits[v] = scale[v] * sum_k fp16(normed_k) * q[v][k] */
-        float* xh = (float*)malloc((size_t)d * 4);
-        for (int k = 0; k < d; k++) xh[k] = orc_f16_to_f32(orc_f32_to_f16(m->normed[k]));
-        for (int v = 0; v < V; v++) {
-            const int8_t* r = m->lm_q + (size_t)v * d;
-            float acc = 0.0f;
-            for (int k = 0; k < d; k++) acc = acc + xh[k] * (float)r[k];
-            m->logits[v] = acc * m->lm_s[v];
-        }
-        free(xh);
+        /* NPU lm_head tiles (reference: src/matmul_decoder.c:1569-1605):
+         * logits[v] = scale[v] * sum_k fp16(normed_k) * q[k][v] */
+        orc_matmul_i8(m->logits, m->normed, m->lm_qt, m->lm_s, 1, d, V);
     } else {
         orc_gemv_rows_f16(m->logits, m->normed, m->lm_f16, V, d);
     }

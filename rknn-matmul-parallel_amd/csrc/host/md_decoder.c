@@ -352,7 +352,11 @@ static int layout(MatmulDecoderContext* c, const md_source* s) {
     CARVE(c->d_tmp, (size_t)(widest > c->d ? widest : c->d) * 4);
     CARVE(c->d_attn16, (size_t)c->qd * 2);
     CARVE(c->d_act16, (size_t)c->F * 2);
-    c->n_partials = mdx_lmhead_partials(nlog);
+    /* partial counts depend on the row count non-monotonically: size for
+     * every lm_head width that can be launched */
+    c->n_partials = mdx_lmhead_partials(c->V);
+    if (c->n_lm && mdx_lmhead_partials(c->lm_vocab) > c->n_partials)
+        c->n_partials = mdx_lmhead_partials(c->lm_vocab);
     CARVE(c->d_partial, (size_t)c->n_partials * 8);
     const int mm = c->max_m;
     const int kmax = c->F > c->qd ? (c->F > c->d ? c->F : c->d) : (c->qd > c->d ? c->qd : c->d);
