@@ -77,16 +77,22 @@ int mdx_debug_gemv(int kind, int K, int N, const void* w, const float* scales, c
 /* M-row MFMA projection, M <= 64: y[M,N] = fp16(x[M,K]) . W (x scale). */
 int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* scales,
                    const float* x, float* y);
-/* One decode attention: q fp32 [nq*hd], cache rows fp16 bits [L][nkv*hd],
- * out fp32 [nq*hd] (the fp16 value the kernel stores, widened). */
-int mdx_debug_attn_decode(int nq, int nkv, int hd, int L, const float* q, const uint16_t* k16,
-                          const uint16_t* v16, float* out);
+/* One decode attention layer at position pos: qkv fp32 [nq*hd + 2*nkv*hd]
+ * (the projection output, before QK-norm and RoPE), cache rows fp16 bits
+ * [pos][nkv*hd] for positions < pos; q_norm/k_norm [hd] may be NULL.
+ * Returns out fp32 [nq*hd] (the fp16 value the kernel stores, widened) and
+ * the appended fp16 K/V row of position pos. */
+int mdx_debug_attn_decode(int nq, int nkv, int hd, int pos, int rope_style, float theta, float eps,
+                          const float* q_norm, const float* k_norm, const float* qkv,
+                          const uint16_t* k16, const uint16_t* v16, float* out, uint16_t* k_new,
+                          uint16_t* v_new);
 /* Causal batch attention of M query rows at positions S..S+M-1 over cache
  * rows [0, S+M) (the batch's own K/V already appended). */
 int mdx_debug_attn_prefill(int nq, int nkv, int hd, int S, int M, const float* q,
                            const uint16_t* k16, const uint16_t* v16, float* out);
-/* QK-norm + RoPE + KV append of one token at position pos: qkv fp32
- * [nq*hd + 2*nkv*hd]; returns q fp32 and the fp16 k,v rows. */
+/* QK-norm + RoPE + KV append of one token at position pos through the
+ * batch-prefill kernel: qkv fp32 [nq*hd + 2*nkv*hd]; returns q fp32 and
+ * the fp16 k,v rows. */
 int mdx_debug_qk_rope(int nq, int nkv, int hd, int pos, int rope_style, float theta, float eps,
                       const float* q_norm, const float* k_norm, const float* qkv, float* q_out,
                       uint16_t* k16, uint16_t* v16);

@@ -134,32 +134,71 @@ static void widen(const uint16_t* h, float* f, size_t n) {
     for (size_t i = 0; i < n; i++) f[i] = mdx_f16_to_f32(h[i]);
 }
 
-int mdx_debug_attn_decode(int nq, int nkv, int hd, int L, const float* q, const uint16_t* k16,
-                          const uint16_t* v16, float* out) {
-    if (nq <= 0 || nkv <= 0 || hd <= 0 || L <= 0 || !q || !k16 || !v16 || !out)
+/* RoPE tables for rows [0, rows) with the reference formula. */
+static int rope_tables(int rows, int hd, float theta, float** ct, float** st) {
+    const int half = hd / 2;
+    *ct = (float*)malloc((size_t)rows * half * 4);
+    *st = (float*)malloc((size_t)rows * half * 4);
+    if (!*ct || !*st) return MATMUL_DECODER_ERR_MEMORY;
+    for (int p = 0; p < rows; p++)
+        for (int i = 0; i < half; i++) {
+            const float freq = 1.0f / powf(theta, (2.0f * i) / hd);
+            const float angle = p * freq;
+            (*ct)[(size_t)p * half + i] = cosf(angle);
+            (*st)[(size_t)p * half + i] = sinf(angle);
+        }
+    return 0;
+}
+
+int mdx_debug_attn_decode(int nq, int nkv, int hd, int pos, int rope_style, float theta, float eps,
+                          const float* q_norm, const float* k_norm, const float* qkv,
+                          const uint16_t* k16, const uint16_t* v16, float* out, uint16_t* k_new,
+                          uint16_t* v_new) {
+    if (nq <= 0 || nkv <= 0 || hd <= 0 || pos < 0 || !qkv || !out || !k_new || !v_new ||
+        (pos > 0 && (!k16 || !v16)))
         return MATMUL_DECODER_ERR_INVALID_ARG;
     dbg_scope s;
     int rc = scope_open(&s);
     if (rc) return rc;
-    const int kvd = nkv * hd, qd = nq * hd;
-    const int max_splits = (L + 15) / 16;
+    const int kvd = nkv * hd, qd = nq * hd, rows = pos + 1, half = hd / 2;
+    const int max_splits = mdx_attn_max_splits(rows);
+    float *ct = NULL, *stt = NULL;
+    rc = rope_tables(rows, hd, theta, &ct, &stt);
     mdx_state* st = NULL;
-    rc = upload_state(&s, L - 1, &st);
-    float* dq = (float*)dalloc(&s, (size_t)qd * 4);
-    uint16_t* dk = (uint16_t*)dalloc(&s, (size_t)L * kvd * 2);
-    uint16_t* dv = (uint16_t*)dalloc(&s, (size_t)L * kvd * 2);
-    float* part = (float*)dalloc(&s, mdx_attn_decode_scratch_floats(nq, hd, max_splits) * 4);
+    if (!rc) rc = upload_state(&s, pos, &st);
+    const size_t scr = mdx_attn_decode_scratch_bytes(nq, nkv, hd, max_splits);
+    float* dcos = (float*)dalloc(&s, (size_t)rows * half * 4);
+    float* dsin = (float*)dalloc(&s, (size_t)rows * half * 4);
+    float* dqkv = (float*)dalloc(&s, (size_t)(qd + 2 * kvd) * 4);
+    uint16_t* dk = (uint16_t*)dalloc(&s, (size_t)rows * kvd * 2);
+    uint16_t* dv = (uint16_t*)dalloc(&s, (size_t)rows * kvd * 2);
+    void* dscr = dalloc(&s, scr);
     uint16_t* o16 = (uint16_t*)dalloc(&s, (size_t)qd * 2);
-    if (!rc && (!dq || !dk || !dv || !part || !o16)) rc = MATMUL_DECODER_ERR_MEMORY;
-    if (!rc) rc = mdxrt_h2d(dq, q, (size_t)qd * 4);
-    if (!rc) rc = mdxrt_h2d(dk, k16, (size_t)L * kvd * 2);
-    if (!rc) rc = mdxrt_h2d(dv, v16, (size_t)L * kvd * 2);
-    if (!rc) rc = mdx_launch_attn_decode(st, dq, dk, dv, nq, nkv, hd, L, max_splits, part, o16, s.stream);
+    float* dqn = q_norm ? (float*)dalloc(&s, (size_t)hd * 4) : NULL;
+    float* dkn = k_norm ? (float*)dalloc(&s, (size_t)hd * 4) : NULL;
+    if (!rc && (!dcos || !dsin || !dqkv || !dk || !dv || !dscr || !o16 || (q_norm && !dqn) ||
+                (k_norm && !dkn)))
+        rc = MATMUL_DECODER_ERR_MEMORY;
+    if (!rc) rc = mdxrt_fill_u32(dscr, 0u, scr / 4, s.stream);
+    if (!rc) rc = mdxrt_h2d(dcos, ct, (size_t)rows * half * 4);
+    if (!rc) rc = mdxrt_h2d(dsin, stt, (size_t)rows * half * 4);
+    if (!rc) rc = mdxrt_h2d(dqkv, qkv, (size_t)(qd + 2 * kvd) * 4);
+    if (!rc && pos > 0) rc = mdxrt_h2d(dk, k16, (size_t)pos * kvd * 2);
+    if (!rc && pos > 0) rc = mdxrt_h2d(dv, v16, (size_t)pos * kvd * 2);
+    if (!rc && dqn) rc = mdxrt_h2d(dqn, q_norm, (size_t)hd * 4);
+    if (!rc && dkn) rc = mdxrt_h2d(dkn, k_norm, (size_t)hd * 4);
+    if (!rc)
+        rc = mdx_launch_attn_decode(st, dqkv, dqn, dkn, eps, dcos, dsin, rope_style, nq, nkv, hd, rows,
+                                    max_splits, dk, dv, dscr, o16, s.stream);
     if (!rc) rc = mdxrt_stream_sync(s.stream);
     uint16_t* h = (uint16_t*)malloc((size_t)qd * 2);
     if (!rc) rc = h ? mdxrt_d2h(h, o16, (size_t)qd * 2) : MATMUL_DECODER_ERR_MEMORY;
     if (!rc) widen(h, out, (size_t)qd);
+    if (!rc) rc = mdxrt_d2h(k_new, dk + (size_t)pos * kvd, (size_t)kvd * 2);
+    if (!rc) rc = mdxrt_d2h(v_new, dv + (size_t)pos * kvd, (size_t)kvd * 2);
     free(h);
+    free(ct);
+    free(stt);
     return scope_close(&s, rc);
 }
 
@@ -199,16 +238,8 @@ int mdx_debug_qk_rope(int nq, int nkv, int hd, int pos, int rope_style, float th
     int rc = scope_open(&s);
     if (rc) return rc;
     const int kvd = nkv * hd, qd = nq * hd, half = hd / 2, rows = pos + 1;
-    float* ct = (float*)malloc((size_t)rows * half * 4);
-    float* stt = (float*)malloc((size_t)rows * half * 4);
-    if (!ct || !stt) rc = MATMUL_DECODER_ERR_MEMORY;
-    for (int p = 0; !rc && p < rows; p++)
-        for (int i = 0; i < half; i++) {
-            const float freq = 1.0f / powf(theta, (2.0f * i) / hd);
-            const float angle = p * freq;
-            ct[(size_t)p * half + i] = cosf(angle);
-            stt[(size_t)p * half + i] = sinf(angle);
-        }
+    float *ct = NULL, *stt = NULL;
+    rc = rope_tables(rows, hd, theta, &ct, &stt);
     mdx_state* st = NULL;
     if (!rc) rc = upload_state(&s, pos, &st);
     float* dcos = (float*)dalloc(&s, (size_t)rows * half * 4);
@@ -227,8 +258,8 @@ int mdx_debug_qk_rope(int nq, int nkv, int hd, int pos, int rope_style, float th
     if (!rc && dqn) rc = mdxrt_h2d(dqn, q_norm, (size_t)hd * 4);
     if (!rc && dkn) rc = mdxrt_h2d(dkn, k_norm, (size_t)hd * 4);
     if (!rc)
-        rc = mdx_launch_qk_rope_append(st, dqkv, dqn, dkn, eps, dcos, dsin, nq, nkv, hd, rope_style,
-                                       dq, dk, dv, s.stream);
+        rc = mdx_launch_qk_rope_append_rows(st, dqkv, 1, dqn, dkn, eps, dcos, dsin, nq, nkv, hd,
+                                            rope_style, dq, dk, dv, s.stream);
     if (!rc) rc = mdxrt_stream_sync(s.stream);
     if (!rc) rc = mdxrt_d2h(q_out, dq, (size_t)qd * 4);
     if (!rc) rc = mdxrt_d2h(k16, dk + (size_t)pos * kvd, (size_t)kvd * 2);
@@ -256,10 +287,11 @@ int mdx_debug_lmhead(int lm_kind, int K, int N, const void* w_rows, const float*
     float* dh = (float*)dalloc(&s, (size_t)K * 4);
     float* dn = (float*)dalloc(&s, (size_t)K * 4);
     float* dl = (float*)dalloc(&s, (size_t)N * 4);
-    void* dp = dalloc(&s, (size_t)mdx_lmhead_partials(N) * 8);
+    void* dp = dalloc(&s, mdx_lmhead_scratch_bytes());
     mdx_state* st = NULL;
     rc = upload_state(&s, 0, &st);
     if (!rc && (!dw || (scales && !ds) || !dh || !dn || !dl || !dp)) rc = MATMUL_DECODER_ERR_MEMORY;
+    if (!rc) rc = mdxrt_fill_u32(dp, 0u, mdx_lmhead_scratch_bytes() / 4, s.stream);
     if (!rc) rc = mdxrt_h2d(dw, w_rows, bytes);
     if (!rc && scales) rc = mdxrt_h2d(ds, scales, (size_t)N * 4);
     if (!rc) rc = mdxrt_h2d(dh, hidden, (size_t)K * 4);
@@ -267,8 +299,7 @@ int mdx_debug_lmhead(int lm_kind, int K, int N, const void* w_rows, const float*
     d.w = dw;
     d.scale = (const float*)ds;
     d.kind = lm_kind == 1 ? MDX_W_I8 : (lm_kind == 3 ? MDX_W_F32 : MDX_W_F16);
-    if (!rc) rc = mdx_launch_lmhead(dh, dn, eps, &d, dl, dp, s.stream);
-    if (!rc) rc = mdx_launch_argmax_finish(st, dp, mdx_lmhead_partials(N), NULL, 0, s.stream);
+    if (!rc) rc = mdx_launch_lmhead(dh, dn, eps, &d, dl, dp, st, NULL, 0, s.stream);
     if (!rc) rc = mdxrt_stream_sync(s.stream);
     if (!rc) rc = mdxrt_d2h(logits, dl, (size_t)N * 4);
     mdx_state h;

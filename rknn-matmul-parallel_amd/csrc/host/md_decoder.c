@@ -49,10 +49,10 @@ struct MatmulDecoderContext {
     md_layer* layers;
     uint16_t *d_kc, *d_vc;
     float *d_cos, *d_sin;
-    float *d_hidden, *d_emb_in, *d_qkv, *d_q, *d_part, *d_logits, *d_tmp;
+    float *d_hidden, *d_emb_in, *d_qkv, *d_logits, *d_tmp;
+    void* d_part;            /* attention split partials + merge counters */
     uint16_t *d_attn16, *d_act16;
-    void* d_partial;
-    int n_partials;
+    void* d_partial;         /* lm_head argmax key + completion counter */
     int* d_tokens;
     int tokens_cap;
     float *d_bhidden, *d_bqkv, *d_bq, *d_gscr;
@@ -62,6 +62,7 @@ struct MatmulDecoderContext {
     md_pgraph pgraphs[4];
     int pgraph_next;
     int capture_M;
+    int use_graphs;          /* 0 when MDX_GRAPHS=0: same kernels, launched one by one */
     mdx_state* h_state;
     float* h_io;
     size_t h_io_floats;
@@ -346,18 +347,12 @@ static int layout(MatmulDecoderContext* c, const md_source* s) {
     CARVE(c->d_hidden, (size_t)c->d * 4);
     CARVE(c->d_emb_in, (size_t)c->d * 4);
     CARVE(c->d_qkv, (size_t)(c->qd + 2 * c->kvd) * 4);
-    CARVE(c->d_q, (size_t)c->qd * 4);
-    CARVE(c->d_part, mdx_attn_decode_scratch_floats(c->nq, c->hd, c->max_splits) * 4);
+    CARVE(c->d_part, mdx_attn_decode_scratch_bytes(c->nq, c->nkv, c->hd, c->max_splits));
     CARVE(c->d_logits, (size_t)nlog * 4);
     CARVE(c->d_tmp, (size_t)(widest > c->d ? widest : c->d) * 4);
     CARVE(c->d_attn16, (size_t)c->qd * 2);
     CARVE(c->d_act16, (size_t)c->F * 2);
-    /* partial counts depend on the row count non-monotonically: size for
-     * every lm_head width that can be launched */
-    c->n_partials = mdx_lmhead_partials(c->V);
-    if (c->n_lm && mdx_lmhead_partials(c->lm_vocab) > c->n_partials)
-        c->n_partials = mdx_lmhead_partials(c->lm_vocab);
-    CARVE(c->d_partial, (size_t)c->n_partials * 8);
+    CARVE(c->d_partial, mdx_lmhead_scratch_bytes());
     const int mm = c->max_m;
     const int kmax = c->F > c->qd ? (c->F > c->d ? c->F : c->d) : (c->qd > c->d ? c->qd : c->d);
     CARVE(c->d_bhidden, (size_t)mm * c->d * 4);
@@ -499,18 +494,20 @@ static int upload_lm_single(MatmulDecoderContext* c, const float* lm32) {
 /* ------------------------------------------------------------------------ */
 
 static int run_layers(MatmulDecoderContext* c, void* s) {
-    int rc = mdx_launch_embed(c->d_state, c->d_emb, c->d_emb_in, c->d_hidden, c->d, c->V, s);
     const float eps = c->config.rms_eps;
+    int rc = 0;
     for (int l = 0; l < c->L && rc == 0; l++) {
         md_layer* ly = &c->layers[l];
-        rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_qkv, s);
+        if (l == 0)
+            rc = mdx_launch_embed_norm_gemv(c->d_state, c->d_emb, c->d_emb_in, c->V, c->d_hidden,
+                                            ly->in_norm, eps, &ly->qkv, c->d_qkv, s);
+        else
+            rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_qkv, s);
         if (!rc)
-            rc = mdx_launch_qk_rope_append(c->d_state, c->d_qkv, ly->q_norm, ly->k_norm, eps,
-                                           c->d_cos, c->d_sin, c->nq, c->nkv, c->hd,
-                                           c->config.rope_style, c->d_q, ly->kc, ly->vc, s);
-        if (!rc)
-            rc = mdx_launch_attn_decode(c->d_state, c->d_q, ly->kc, ly->vc, c->nq, c->nkv, c->hd,
-                                        c->max_seq, c->max_splits, c->d_part, c->d_attn16, s);
+            rc = mdx_launch_attn_decode(c->d_state, c->d_qkv, ly->q_norm, ly->k_norm, eps, c->d_cos,
+                                        c->d_sin, c->config.rope_style, c->nq, c->nkv, c->hd,
+                                        c->max_seq, c->max_splits, ly->kc, ly->vc, c->d_part,
+                                        c->d_attn16, s);
         if (!rc) rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_hidden, s);
         if (!rc) rc = mdx_launch_norm_gemv(c->d_hidden, ly->post_norm, eps, &ly->gu, 1, c->d_act16, s);
         if (!rc) rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_hidden, s);
@@ -520,11 +517,8 @@ static int run_layers(MatmulDecoderContext* c, void* s) {
 
 static int run_head(MatmulDecoderContext* c, const mdx_wdesc* lm, int* out_tokens, int advance,
                     void* s) {
-    int rc = mdx_launch_lmhead(c->d_hidden, c->d_final_norm, c->config.rms_eps, lm, c->d_logits,
-                               c->d_partial, s);
-    if (!rc) rc = mdx_launch_argmax_finish(c->d_state, c->d_partial, mdx_lmhead_partials(lm->N),
-                                           out_tokens, advance, s);
-    return rc;
+    return mdx_launch_lmhead(c->d_hidden, c->d_final_norm, c->config.rms_eps, lm, c->d_logits,
+                             c->d_partial, c->d_state, out_tokens, advance, s);
 }
 
 static int run_prefill(MatmulDecoderContext* c, int M, void* s) {
@@ -569,8 +563,18 @@ static int seq_greedy(MatmulDecoderContext* c, void* s) {
     return rc;
 }
 
+/* Launches a captured sequence, or issues its kernels directly when graphs
+ * are switched off. */
+static int launch_seq(MatmulDecoderContext* c, void* exec, md_seq_fn fn) {
+    return c->use_graphs ? mdxrt_graph_launch(exec, c->stream) : fn(c, c->stream);
+}
+
 static int ensure_graphs(MatmulDecoderContext* c) {
     if (c->graphs_ready) return 0;
+    if (!c->use_graphs) {
+        c->graphs_ready = 1;
+        return 0;
+    }
     int rc = capture(c, seq_layers, &c->g_layers);
     if (!rc && c->n_lm <= 1) rc = capture(c, seq_head, &c->g_head);
     if (!rc) rc = capture(c, seq_adv, &c->g_adv);
@@ -585,6 +589,7 @@ static int ensure_graphs(MatmulDecoderContext* c) {
 static int seq_prefill(MatmulDecoderContext* c, void* s) { return run_prefill(c, c->capture_M, s); }
 
 static void* prefill_graph(MatmulDecoderContext* c, int M) {
+    if (!c->use_graphs) return NULL;
     for (int i = 0; i < 4; i++)
         if (c->pgraphs[i].exec && c->pgraphs[i].M == M) return c->pgraphs[i].exec;
     md_pgraph* slot = &c->pgraphs[c->pgraph_next];
@@ -658,7 +663,11 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
                           : c->V;
     int mm = config->max_batch_prefill > 0 ? config->max_batch_prefill : 64;
     c->max_m = mm > 64 ? 64 : mm;
-    c->max_splits = (max_seq_len + 15) / 16;
+    c->max_splits = mdx_attn_max_splits(max_seq_len);
+    {
+        const char* e = getenv("MDX_GRAPHS");
+        c->use_graphs = !(e && e[0] == '0');
+    }
     c->layers = (md_layer*)calloc((size_t)c->L, sizeof(md_layer));
     if (c->n_lm) c->lm_heads = (mdx_wdesc*)calloc((size_t)c->n_lm, sizeof(mdx_wdesc));
     if (!c->layers || (c->n_lm && !c->lm_heads)) goto fail;
@@ -863,9 +872,9 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     }
     rc = set_state(c, token_id, embedding);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    if (!rc) rc = mdxrt_graph_launch(c->g_layers, c->stream);
+    if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
-    if (!rc) rc = mdxrt_graph_launch(want_head ? c->g_head : c->g_adv, c->stream);
+    if (!rc) rc = launch_seq(c, want_head ? c->g_head : c->g_adv, want_head ? seq_head : seq_adv);
     if (!rc) rc = mdxrt_event_record(c->ev2, c->stream);
     if (!rc && output_logits) rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
@@ -917,7 +926,7 @@ int matmul_decoder_step_head(MatmulDecoderContext* c, int token_id, const float*
     if (rc) return rc;
     if (ensure_graphs(c)) return MATMUL_DECODER_ERR_RKNN;
     rc = set_state(c, token_id, embedding);
-    if (!rc) rc = mdxrt_graph_launch(c->g_layers, c->stream);
+    if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
     if (!rc) rc = run_head(c, &c->lm_heads[lm_head_idx], NULL, 1, c->stream);
     if (!rc && output_logits)
         rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->lm_vocab * 4, c->stream);
@@ -1092,13 +1101,14 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
         if (mdxrt_malloc((void**)&c->d_tokens, (size_t)cap * 4)) return MATMUL_DECODER_ERR_MEMORY;
         c->tokens_cap = cap;
     }
-    if (!c->g_greedy && capture(c, seq_greedy, &c->g_greedy)) return MATMUL_DECODER_ERR_RKNN;
+    if (c->use_graphs && !c->g_greedy && capture(c, seq_greedy, &c->g_greedy))
+        return MATMUL_DECODER_ERR_RKNN;
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
     c->h_state->token = first_token;
     int rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    for (int i = 0; i < n_steps && !rc; i++) rc = mdxrt_graph_launch(c->g_greedy, c->stream);
+    for (int i = 0; i < n_steps && !rc; i++) rc = launch_seq(c, c->g_greedy, seq_greedy);
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
     if (!rc) rc = mdxrt_d2h(out_tokens, c->d_tokens, (size_t)n_steps * 4);
@@ -1130,7 +1140,7 @@ int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, f
             case 3: rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream); break;
             default:
                 rc = mdx_launch_lmhead(c->d_hidden, c->d_final_norm, eps, w0, c->d_logits,
-                                       c->d_partial, c->stream);
+                                       c->d_partial, c->d_state, NULL, 0, c->stream);
         }
     }
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
@@ -1158,7 +1168,7 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
     if (!c || !embeddings || M <= 0 || M > c->max_m || iters <= 0) return MATMUL_DECODER_ERR_INVALID_ARG;
     if (c->seq_len + M > c->max_seq) return MATMUL_DECODER_ERR_INVALID_ARG;
     void* g = prefill_graph(c, M);
-    if (!g) return MATMUL_DECODER_ERR_RKNN;
+    if (!g && c->use_graphs) return MATMUL_DECODER_ERR_RKNN;
     memcpy(c->h_io, embeddings, (size_t)M * c->d * 4);
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
@@ -1166,7 +1176,7 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
     for (int i = 0; i < iters && !rc; i++) {
         rc = mdxrt_h2d_async(c->d_bhidden, c->h_io, (size_t)M * c->d * 4, c->stream);
         if (!rc) rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
-        if (!rc) rc = mdxrt_graph_launch(g, c->stream);
+        if (!rc) rc = g ? mdxrt_graph_launch(g, c->stream) : run_prefill(c, M, c->stream);
     }
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);

@@ -28,6 +28,23 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
+// Data exchanged between workgroups of one kernel goes through agent-coherent
+// 32-bit accesses (relaxed agent-scope atomics): they bypass the per-XCD L2,
+// so no device-wide cache write-back / invalidate (fence) is needed.  The
+// writer waits for its stores to complete (wait_all) before it signals with
+// an atomic; the reader only loads after it has observed that signal.
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_coherent_u32(const unsigned* p) {
+    return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every memory operation this thread issued has completed.
+__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Sum over all 64 lanes; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

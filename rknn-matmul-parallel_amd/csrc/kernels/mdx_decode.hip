@@ -3,11 +3,17 @@
 // Projections (reference: src/matmul_decoder.c:382-445, the NPU call sites
 // K1/K2; CPU GEMVs :511-616) run as bandwidth-bound GEMVs over the W^T
 // device layout: each wave owns RW weight rows, every lane streams 16-byte
-// chunks of each row (so one wave load instruction reads 1 KiB contiguous),
-// dequantises in registers, accumulates with v_dot2_f32_f16 and the wave
-// reduces with lane shuffles.  The activation vector is built once per
-// workgroup in LDS, fused with the RMSNorm that precedes it in the layer
-// (reference: src/cpu_ops.c:18-55).
+// chunks of each row (one wave load instruction reads 1 KiB contiguous),
+// dequantises in registers, accumulates with v_dot2_f32_f16 and reduces with
+// lane shuffles.  The weight loads are issued before the activation prologue
+// (they do not depend on it), so HBM latency overlaps the RMSNorm that
+// builds the fp16 activation vector in LDS (reference: src/cpu_ops.c:18-55).
+//
+// Attention (reference: src/cpu_ops.c:202-264 and the QK-norm/RoPE/KV-append
+// steps of src/matmul_decoder.c:1493-1520) is one kernel per layer: every
+// block normalises and rotates its query heads itself, the block holding the
+// newest position appends that position's K/V to the fp16 cache, blocks
+// split the positions, and the last block to finish merges the splits.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -20,32 +26,37 @@ using namespace mdx;
 
 namespace {
 
-enum XMode { XM_NORM = 0, XM_F16 = 1, XM_F32 = 2 };
+enum XMode { XM_NORM = 0, XM_F16 = 1, XM_F32 = 2, XM_EMBED = 3 };
 enum Epi { EP_STORE = 0, EP_ADD = 1, EP_SWIGLU = 2, EP_LOGITS = 3 };
 // KF16/KI8/KI4: fp16 activations (the NPU input).  KF32X: fp32 rows with fp32
 // activations, KF16X: fp16 rows with fp32 activations (the CPU GEMVs).
 enum Kind { KF16 = 0, KI8 = 1, KI4 = 2, KF32X = 3, KF16X = 4 };
 
-struct ArgPair {
-    float v;
-    int i;
-};
-
 struct GemvArgs {
     const uint8_t* w;
     const float* scale;
     int K, N;             // N weight rows
-    int n_units;          // output units; unit u uses rows u (and u + n_units when unit_rows == 2)
+    int n_units;          // unit u uses rows u (and u + n_units when unit_rows == 2)
     int unit_rows;
     int xmode;
-    const float* xf32;
+    const float* xf32;    // XM_NORM/XM_F32 input, XM_EMBED uploaded embedding
     const uint16_t* x16;
     const float* norm_w;
     float eps;
     int epi;
     float* out_f32;
     uint16_t* out_f16;
-    ArgPair* partial;
+    // XM_EMBED: input row chosen by state->mode / state->token, copied to hidden_out
+    const mdx_state* st_in;
+    const float* emb_table;
+    int vocab;
+    float* hidden_out;
+    // EP_LOGITS: fused argmax and step bookkeeping
+    mdx_state* st;
+    unsigned long long* amax_key;
+    unsigned int* done;
+    int* out_tokens;
+    int advance;
 };
 
 template <int KIND> struct KindTraits;
@@ -54,7 +65,7 @@ template <> struct KindTraits<KI8> { static constexpr int E = 16; static constex
 template <> struct KindTraits<KI4> { static constexpr int E = 32; static constexpr bool XF32 = false; static constexpr int EB2 = 1; };
 template <> struct KindTraits<KF32X> { static constexpr int E = 4; static constexpr bool XF32 = true; static constexpr int EB2 = 8; };
 template <> struct KindTraits<KF16X> { static constexpr int E = 8; static constexpr bool XF32 = true; static constexpr int EB2 = 4; };
-// EB2 = row bytes per element, times 2 (int4 rows hold half a byte per element).
+// E = elements per 16-byte chunk; EB2 = row bytes per element, times 2.
 
 template <int KIND>
 __device__ __forceinline__ float chunk_dot(uint4 w, const uint4* xs, int j, float acc) {
@@ -96,16 +107,27 @@ __device__ __forceinline__ float chunk_dot(uint4 w, const uint4* xs, int j, floa
 }
 
 // Builds the activation vector in LDS: fp16 for the NPU-style kinds, fp32 for
-// the CPU-GEMV kinds.  XM_NORM applies the reference RMSNorm first.
+// the CPU-GEMV kinds.  XM_NORM / XM_EMBED apply the reference RMSNorm first.
 template <bool XF32>
 __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* red) {
     const int tid = threadIdx.x;
     const int K = a.K;
+    const float* src = a.xf32;
+    if (a.xmode == XM_EMBED) {
+        if (a.st_in->mode != 1) {
+            int tok = a.st_in->token;
+            tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
+            src = a.emb_table + (size_t)tok * K;
+        }
+        if (blockIdx.x == 0)
+            for (int k = tid; k < K; k += blockDim.x) a.hidden_out[k] = src[k];
+    }
+    const bool norm = a.xmode == XM_NORM || a.xmode == XM_EMBED;
     float rms = 1.0f;
-    if (a.xmode == XM_NORM) {
+    if (norm) {
         float ss = 0.0f;
         for (int k = tid; k < K; k += blockDim.x) {
-            float v = a.xf32[k];
+            const float v = src[k];
             ss += v * v;
         }
         ss = wave_sum(ss);
@@ -119,126 +141,176 @@ __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* 
         float* xs = reinterpret_cast<float*>(xs_raw);
         for (int k = tid; k < K; k += blockDim.x) {
             float v;
-            if (a.xmode == XM_NORM) v = (a.xf32[k] * rms) * a.norm_w[k];
+            if (norm) v = (src[k] * rms) * a.norm_w[k];
             else if (a.xmode == XM_F16) v = f16_bits_to_f32(a.x16[k]);
-            else v = a.xf32[k];
+            else v = src[k];
             xs[k] = v;
         }
     } else {
         uint16_t* xs = reinterpret_cast<uint16_t*>(xs_raw);
         for (int k = tid; k < K; k += blockDim.x) {
             uint16_t v;
-            if (a.xmode == XM_NORM) v = f32_to_f16_bits((a.xf32[k] * rms) * a.norm_w[k]);
+            if (norm) v = f32_to_f16_bits((src[k] * rms) * a.norm_w[k]);
             else if (a.xmode == XM_F16) v = a.x16[k];
-            else v = f32_to_f16_bits(a.xf32[k]);
+            else v = f32_to_f16_bits(src[k]);
             xs[k] = v;
         }
     }
     __syncthreads();
 }
 
-// The GEMV.  grid.x = ceil(n_units * unit_rows / (4 * RW)), block = 256.
+// Order-preserving key: larger value wins, equal values pick the lower index
+// (reference argmax: strict >, first index of the maximum).
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
+}
+
+template <int KIND, int RW, int U>
+struct RowSet {
+    int rows[RW];
+    bool valid[RW];
+    __device__ __forceinline__ void init(const GemvArgs& a, int blk, int wave) {
+        const int slot0 = (blk * 4 + wave) * RW;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int slot = slot0 + r;
+            const int unit = slot / a.unit_rows, which = slot % a.unit_rows;
+            valid[r] = unit < a.n_units;
+            rows[r] = unit + which * a.n_units;
+        }
+    }
+    __device__ __forceinline__ void load(const GemvArgs& a, size_t row_bytes, int nchunks, int base,
+                                         int lane, uint4 (&wv)[RW][U]) const {
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const uint4* rp = reinterpret_cast<const uint4*>(a.w + (size_t)rows[r] * row_bytes);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int j = base + u * 64 + lane;
+                wv[r][u] = (valid[r] && j < nchunks) ? rp[j] : make_uint4(0, 0, 0, 0);
+            }
+        }
+    }
+};
+
+// The GEMV.  Blocks of 256 threads (4 waves x RW rows) walk the row blocks
+// with a grid stride; the next row block's weights are requested before the
+// current one is reduced.
 template <int KIND, int RW, int U>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     using T = KindTraits<KIND>;
     extern __shared__ uint4 xs[];
     __shared__ float red[4];
-    __shared__ ArgPair amax[4];
-
-    build_x<T::XF32>(a, xs, red);
+    __shared__ unsigned long long bkey[4];
+    __shared__ int last_block;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int nchunks = a.K / T::E;
     const size_t row_bytes = (size_t)a.K * T::EB2 / 2;
-    const int ru = a.unit_rows;
-    const int slot0 = (blockIdx.x * 4 + wave) * RW;   // first row slot of this wave
+    const long slots = (long)a.n_units * a.unit_rows;
+    const int nblk = (int)((slots + 4L * RW - 1) / (4L * RW));
+    const bool single = nchunks <= 64 * U;
 
-    int rows[RW];
-    bool valid[RW];
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-        const int slot = slot0 + r;
-        const int unit = slot / ru, which = slot % ru;
-        valid[r] = unit < a.n_units;
-        rows[r] = unit + which * a.n_units;
+    int blk = blockIdx.x;
+    RowSet<KIND, RW, U> rs;
+    uint4 wv[RW][U];
+    if (blk < nblk) {
+        rs.init(a, blk, wave);
+        rs.load(a, row_bytes, nchunks, 0, lane, wv);
     }
+    build_x<T::XF32>(a, xs, red);
 
-    float acc[RW];
+    unsigned long long best = 0ull;
+    for (; blk < nblk; blk += gridDim.x) {
+        float acc[RW];
 #pragma unroll
-    for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+        for (int r = 0; r < RW; r++) acc[r] = 0.0f;
+        for (int base = 0; base < nchunks; base += 64 * U) {
+            if (base > 0) rs.load(a, row_bytes, nchunks, base, lane, wv);
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int j = base + u * 64 + lane;
+                    if (j < nchunks) acc[r] = chunk_dot<KIND>(wv[r][u], xs, j, acc[r]);
+                }
+        }
+        RowSet<KIND, RW, U> cur = rs;
+        const int nb = blk + gridDim.x;
+        if (nb < nblk) {                    // request the next row block now
+            rs.init(a, nb, wave);
+            if (single) rs.load(a, row_bytes, nchunks, 0, lane, wv);
+        }
 
-    for (int base = 0; base < nchunks; base += 64 * U) {
-        uint4 wv[RW][U];
+        float y[RW];
 #pragma unroll
         for (int r = 0; r < RW; r++) {
-            const uint8_t* rp = a.w + (size_t)rows[r] * row_bytes;
+            y[r] = wave_sum(acc[r]);
+            if (a.scale && cur.valid[r]) y[r] = y[r] * a.scale[cur.rows[r]];
+        }
+        if (a.epi == EP_SWIGLU) {
+            // slots come in (gate, up) pairs: slot 2c is row unit, 2c+1 row unit + F
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int j = base + u * 64 + lane;
-                if (valid[r] && j < nchunks)
-                    wv[r][u] = reinterpret_cast<const uint4*>(rp)[j];
-                else
-                    wv[r][u] = make_uint4(0, 0, 0, 0);
+            for (int r = 0; r + 1 < RW; r += 2) {
+                if (cur.valid[r] && lane == r) {
+                    const int unit = cur.rows[r];
+                    const float g = y[r], u = y[r + 1];
+                    float v;
+                    if (unit < (a.n_units & ~3)) v = silu_mul(g, u);
+                    else v = (g / (1.0f + expf(-g))) * u;     // reference tail formula
+                    a.out_f16[unit] = f32_to_f16_bits(v);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                if (cur.valid[r] && lane == r) {
+                    if (a.epi == EP_ADD) a.out_f32[cur.rows[r]] = a.out_f32[cur.rows[r]] + y[r];
+                    else a.out_f32[cur.rows[r]] = y[r];
+                }
             }
         }
+        if (a.epi == EP_LOGITS) {
 #pragma unroll
-        for (int r = 0; r < RW; r++) {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int j = base + u * 64 + lane;
-                if (j < nchunks) acc[r] = chunk_dot<KIND>(wv[r][u], xs, j, acc[r]);
+            for (int r = 0; r < RW; r++) {
+                if (cur.valid[r] && y[r] == y[r]) {
+                    const unsigned long long k = argmax_key(y[r], cur.rows[r]);
+                    if (k > best) best = k;
+                }
             }
         }
-    }
-
-    float y[RW];
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-        y[r] = wave_sum(acc[r]);
-        if (a.scale && valid[r]) y[r] = y[r] * a.scale[rows[r]];
-    }
-
-    if (a.epi == EP_STORE || a.epi == EP_ADD || a.epi == EP_LOGITS) {
-#pragma unroll
-        for (int r = 0; r < RW; r++) {
-            if (valid[r] && lane == (r & 63)) {
-                if (a.epi == EP_ADD) a.out_f32[rows[r]] = a.out_f32[rows[r]] + y[r];
-                else a.out_f32[rows[r]] = y[r];
-            }
-        }
-    } else if (a.epi == EP_SWIGLU) {
-        // slots come in (gate, up) pairs: slot 2c is row unit, slot 2c+1 is row unit + F
-#pragma unroll
-        for (int r = 0; r + 1 < RW; r += 2) {
-            if (valid[r] && lane == (r & 63)) {
-                const int unit = rows[r];
-                const float g = y[r], u = y[r + 1];
-                float v;
-                if (unit < (a.n_units & ~3)) v = silu_mul(g, u);
-                else v = (g / (1.0f + expf(-g))) * u;     // reference tail formula
-                a.out_f16[unit] = f32_to_f16_bits(v);
-            }
-        }
+        if (!single && nb < nblk) rs.load(a, row_bytes, nchunks, 0, lane, wv);
     }
 
     if (a.epi == EP_LOGITS) {
-        ArgPair best = {-INFINITY, -1};
-#pragma unroll
-        for (int r = 0; r < RW; r++) {
-            if (valid[r] && (y[r] > best.v || best.i < 0)) {
-                if (!(y[r] != y[r])) { best.v = y[r]; best.i = rows[r]; }
-            }
-        }
-        if (lane == 0) amax[wave] = best;
+        if (lane == 0) bkey[wave] = best;
         __syncthreads();
         if (tid == 0) {
-            ArgPair b = amax[0];
-            for (int wv = 1; wv < 4; wv++) {
-                const ArgPair c = amax[wv];
-                if (c.i >= 0 && (b.i < 0 || c.v > b.v)) b = c;
+            unsigned long long b = bkey[0];
+            for (int w = 1; w < 4; w++) b = bkey[w] > b ? bkey[w] : b;
+            if (b) atomicMax(a.amax_key, b);
+            __threadfence();
+            const unsigned prev = atomicAdd(a.done, 1u);
+            last_block = prev == gridDim.x - 1;
+        }
+        __syncthreads();
+        if (last_block && tid == 0) {
+            __threadfence();
+            const unsigned long long k = atomicExch(a.amax_key, 0ull);
+            atomicExch(a.done, 0u);
+            const int tok = k ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+            mdx_state* st = a.st;
+            st->argmax = tok;
+            st->token = tok;
+            st->mode = 0;
+            if (a.out_tokens) {
+                a.out_tokens[st->n_out] = tok;
+                st->n_out = st->n_out + 1;
             }
-            a.partial[blockIdx.x] = b;
+            st->pos = st->pos + a.advance;
         }
     }
 }
@@ -247,12 +319,14 @@ typedef void (*GemvKernel)(GemvArgs);
 
 template <int KIND>
 GemvKernel pick_kernel(int rw, int u) {
-#define MDX_U_CASES(RW_)                                        \
-    switch (u) {                                                \
-        case 1: return k_gemv<KIND, RW_, 1>;                    \
-        case 2: return k_gemv<KIND, RW_, 2>;                    \
-        case 4: return k_gemv<KIND, RW_, 4>;                    \
-        default: return k_gemv<KIND, RW_, 8>;                   \
+#define MDX_U_CASES(RW_)                               \
+    switch (u) {                                       \
+        case 1: return k_gemv<KIND, RW_, 1>;           \
+        case 2: return k_gemv<KIND, RW_, 2>;           \
+        case 3: return k_gemv<KIND, RW_, 3>;           \
+        case 4: return k_gemv<KIND, RW_, 4>;           \
+        case 6: return k_gemv<KIND, RW_, 6>;           \
+        default: return k_gemv<KIND, RW_, 8>;          \
     }
     switch (rw) {
         case 1: MDX_U_CASES(1)
@@ -283,22 +357,35 @@ int elems_per_chunk(int kind) {
     }
 }
 
-int pow2_at_least(int v, int cap) {
-    int p = 1;
-    while (p < v && p < cap) p <<= 1;
-    return p;
+// chunks per lane per round: the smallest of {1,2,3,4,6,8} covering the row,
+// with at most 16 outstanding 16-byte loads per lane (RW*U <= 16).
+int pick_u(int nchunks, int rw) {
+    static const int opts[6] = {1, 2, 3, 4, 6, 8};
+    const int need = (nchunks + 63) / 64;
+    int cap = 16 / rw;
+    int best = 1;
+    for (int i = 0; i < 6; i++) {
+        if (opts[i] > cap) break;
+        best = opts[i];
+        if (opts[i] >= need) break;
+    }
+    return best;
 }
 
-// rows_per_wave: how many weight rows one wave streams at once.
-int launch_gemv(int kind, GemvArgs a, int rows_per_wave, void* stream) {
+int rows_per_wave_for(int rows) {
+    if (rows >= 65536) return 8;
+    if (rows >= 4096) return 2;
+    return 1;
+}
+
+int launch_gemv(int kind, GemvArgs a, int rw, int max_grid, void* stream) {
     const int E = elems_per_chunk(kind);
     if (a.K <= 0 || a.K % E != 0 || a.n_units <= 0) return -1;
     const int nchunks = a.K / E;
-    const int rw = rows_per_wave;
-    // at most 16 outstanding 16-byte loads per lane (64 VGPRs of weights)
-    const int u = pow2_at_least((nchunks + 63) / 64, 16 / rw < 8 ? 16 / rw : 8);
+    const int u = pick_u(nchunks, rw);
     const long slots = (long)a.n_units * a.unit_rows;
-    const long grid = (slots + 4L * rw - 1) / (4L * rw);
+    long grid = (slots + 4L * rw - 1) / (4L * rw);
+    if (max_grid > 0 && grid > max_grid) grid = max_grid;
     const bool xf32 = kind == KF32X || kind == KF16X;
     const size_t lds = (size_t)a.K * (xf32 ? 4 : 2);
     if (lds > 64 * 1024) return -5;
@@ -316,46 +403,52 @@ int kind_from(const mdx_wdesc* w, int x_fp32_exact) {
     }
 }
 
-// Rows per wave chosen so that a launch has enough waves in flight for HBM.
-int rows_per_wave_for(int kind, int units_rows, int K) {
-    (void)K;
-    if (units_rows >= 65536) return 8;
-    if (units_rows >= 4096) return 2;
-    return 1;
+GemvArgs base_args(const mdx_wdesc* w) {
+    GemvArgs a = {};
+    a.w = (const uint8_t*)w->w;
+    a.scale = w->scale;
+    a.K = w->K;
+    a.N = w->N;
+    a.n_units = w->N;
+    a.unit_rows = 1;
+    return a;
 }
 
-__global__ void k_embed(const mdx_state* st, const float* table, const float* emb_in,
-                        float* hidden, int d, int vocab) {
-    const int mode = st->mode;
-    int tok = st->token;
-    if (tok < 0) tok = 0;
-    if (tok >= vocab) tok = vocab - 1;
-    const float* src = mode == 1 ? emb_in : table + (size_t)tok * d;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
-        hidden[i] = src[i];
+// ---- attention ---------------------------------------------------------------
+
+struct AttnArgs {
+    const mdx_state* st;
+    const float* qkv;         // [nq*hd | nkv*hd | nkv*hd] fp32 projection output
+    const float* q_norm;
+    const float* k_norm;
+    float eps;
+    const float* cos_t;
+    const float* sin_t;
+    int style;
+    uint16_t* kc;             // layer cache [max_seq][nkv*hd] fp16
+    uint16_t* vc;
+    int nkv;
+    int max_splits;
+    int chunk_cap;
+    float* part;              // [nkv][max_splits][G][hd + 2]
+    unsigned int* done;       // [nkv], zero between launches
+    uint16_t* out16;          // [nq*hd]
+};
+
+__device__ __forceinline__ void attn_plan(int L, int max_splits, int& splits, int& chunk) {
+    int s = (L + 15) / 16;
+    if (s > max_splits) s = max_splits;
+    chunk = (L + s - 1) / s;
+    splits = (L + chunk - 1) / chunk;
 }
 
-// QK-norm + RoPE + KV append for one token (reference:
-// src/matmul_decoder.c:1493-1516).  grid = nq + 2*nkv waves: q heads, k heads,
-// then v heads.
-__global__ __launch_bounds__(64) void k_qk_rope_append(
-    const mdx_state* st, const float* qkv, const float* q_norm, const float* k_norm, float eps,
-    const float* cos_t, const float* sin_t, int nq, int nkv, int hd, int style, float* q_out,
-    uint16_t* k_cache, uint16_t* v_cache) {
-    const int b = blockIdx.x, lane = threadIdx.x;
-    const int pos = st->pos;
+// Per-head RMSNorm (optional) + RoPE of one head vector, one wave.  Writes the
+// rotated fp32 values to dst (LDS) and, when cache != NULL, their fp16
+// roundings to cache (and the rounded values to dst, the fp16 KV semantic).
+__device__ __forceinline__ void rope_head(const float* src, const float* nw, float eps,
+                                          const float* cr, const float* sr, int hd, int style,
+                                          float* dst, uint16_t* cache, int lane) {
     const int half = hd / 2;
-    const int qd = nq * hd, kvd = nkv * hd;
-    if (b >= nq + nkv) {
-        const int h = b - nq - nkv;
-        const float* src = qkv + qd + kvd + h * hd;
-        uint16_t* dst = v_cache + (size_t)pos * kvd + h * hd;
-        for (int e = lane; e < hd; e += 64) dst[e] = f32_to_f16_bits(src[e]);
-        return;
-    }
-    const bool is_q = b < nq;
-    const float* src = is_q ? qkv + b * hd : qkv + qd + (b - nq) * hd;
-    const float* nw = is_q ? q_norm : k_norm;
     float rms = 1.0f;
     if (nw) {
         float ss = 0.0f;
@@ -363,8 +456,6 @@ __global__ __launch_bounds__(64) void k_qk_rope_append(
         ss = wave_sum(ss);
         rms = 1.0f / sqrtf(ss / (float)hd + eps);
     }
-    const float* cr = cos_t + (size_t)pos * half;
-    const float* sr = sin_t + (size_t)pos * half;
     for (int i = lane; i < half; i += 64) {
         const int i0 = style == 0 ? 2 * i : i;
         const int i1 = style == 0 ? 2 * i + 1 : i + half;
@@ -374,125 +465,173 @@ __global__ __launch_bounds__(64) void k_qk_rope_append(
             x1 = (x1 * rms) * nw[i1];
         }
         const float c = cr[i], s = sr[i];
-        const float o0 = x0 * c - x1 * s;
-        const float o1 = x1 * c + x0 * s;
-        if (is_q) {
-            q_out[b * hd + i0] = o0;
-            q_out[b * hd + i1] = o1;
-        } else {
-            uint16_t* dst = k_cache + (size_t)pos * kvd + (b - nq) * hd;
-            dst[i0] = f32_to_f16_bits(o0);
-            dst[i1] = f32_to_f16_bits(o1);
+        float o0 = x0 * c - x1 * s;
+        float o1 = x1 * c + x0 * s;
+        if (cache) {
+            const uint16_t h0 = f32_to_f16_bits(o0), h1 = f32_to_f16_bits(o1);
+            cache[i0] = h0;
+            cache[i1] = h1;
+            o0 = f16_bits_to_f32(h0);
+            o1 = f16_bits_to_f32(h1);
         }
+        dst[i0] = o0;
+        dst[i1] = o1;
     }
 }
 
-__device__ __forceinline__ void split_plan(int L, int max_splits, int& splits, int& chunk) {
-    splits = (L + 15) / 16;
-    if (splits > max_splits) splits = max_splits;
-    if (splits < 1) splits = 1;
-    chunk = (L + splits - 1) / splits;
-}
-
-// Split-K decode attention (reference: src/cpu_ops.c:202-264).  grid =
-// (nkv, max_splits), 256 threads.  Each block covers one KV head (all G query
-// heads of its group share the K/V reads) and one range of positions, and
-// writes (max, sum of exp, unnormalised P.V) for each query head.
+// grid = (nkv, max_splits), 256 threads.  Block (h, s) covers positions
+// [s*chunk, min(L, (s+1)*chunk)) of KV head h for its G query heads.
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_split(const mdx_state* st, const float* q,
-                                                    const uint16_t* kc, const uint16_t* vc,
-                                                    int nkv, int max_splits, float* part) {
-    constexpr int LP = HD / 8;          // lanes per position row (16-byte chunks)
-    constexpr int PPW = 64 / LP;        // positions per wave step
-    constexpr int PG = 256 / LP;        // position groups for P.V
+__global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
+    constexpr int LP = HD / 8;          // lanes per position (16-byte chunks)
+    constexpr int PPW = 64 / LP;        // positions per wave per tile
+    constexpr int TILE = 4 * PPW;       // positions per tile
+    constexpr int PG = 256 / LP;        // position groups in P.V
+    constexpr int GD4 = G * HD / 4;     // float4 slices of the G output heads
+    constexpr int SG = 256 / GD4 > 0 ? 256 / GD4 : 1;   // split groups in the merge
     extern __shared__ float smem[];
     float* qs = smem;                   // [G][HD]
-    float* sc = qs + G * HD;            // [G][chunk]
+    float* kn = qs + G * HD;            // [HD] newest K (fp16-rounded)
+    float* vn = kn + HD;                // [HD] newest V (fp16-rounded)
+    float* sc = vn + HD;                // [G][chunk_cap]
     __shared__ float ml[2 * G];
+    __shared__ int is_last;
 
-    const int L = st->pos + 1;
+    const int pos = a.st->pos;
+    const int L = pos + 1;
     int splits, chunk;
-    split_plan(L, max_splits, splits, chunk);
+    attn_plan(L, a.max_splits, splits, chunk);
     const int s = blockIdx.y;
     if (s >= splits) return;
     const int kvh = blockIdx.x;
     const int p0 = s * chunk;
     const int p1 = min(L, p0 + chunk);
     const int n = p1 - p0;
+    const bool has_new = p1 == L;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int kvd = nkv * HD;
+    const int nq = a.nkv * G, qd = nq * HD, kvd = a.nkv * HD;
+    const int half = HD / 2;
     const float scale = 1.0f / sqrtf((float)HD);
+    const int sub = lane % LP, slot = lane / LP;
+    const int dsub = tid % LP, pg = tid / LP;
 
-    for (int i = tid; i < G * HD; i += 256) qs[i] = q[(size_t)kvh * G * HD + i];
+    // first K and V tiles: issue the cache loads before anything else
+    uint4 kpre = make_uint4(0, 0, 0, 0), vpre = make_uint4(0, 0, 0, 0);
+    {
+        const int pk = p0 + wave * PPW + slot;
+        if (wave * PPW + slot < n && pk < pos)
+            kpre = *reinterpret_cast<const uint4*>(a.kc + (size_t)pk * kvd + kvh * HD + sub * 8);
+        const int pv = p0 + pg;
+        if (pg < n && pv < pos)
+            vpre = *reinterpret_cast<const uint4*>(a.vc + (size_t)pv * kvd + kvh * HD + dsub * 8);
+    }
+
+    // QK-norm + RoPE of the G query heads (every block), and of the newest
+    // K/V row (the block that holds position pos, which also appends it)
+    const float* cr = a.cos_t + (size_t)pos * half;
+    const float* sr = a.sin_t + (size_t)pos * half;
+    for (int t = wave; t < G + 2; t += 4) {
+        if (t < G) {
+            rope_head(a.qkv + (size_t)(kvh * G + t) * HD, a.q_norm, a.eps, cr, sr, HD, a.style,
+                      qs + t * HD, nullptr, lane);
+        } else if (has_new && t == G) {
+            rope_head(a.qkv + qd + kvh * HD, a.k_norm, a.eps, cr, sr, HD, a.style, kn,
+                      a.kc + (size_t)pos * kvd + kvh * HD, lane);
+        } else if (has_new) {
+            const float* src = a.qkv + qd + kvd + kvh * HD;
+            uint16_t* dst = a.vc + (size_t)pos * kvd + kvh * HD;
+            for (int e = lane; e < HD; e += 64) {
+                const uint16_t hv = f32_to_f16_bits(src[e]);
+                dst[e] = hv;
+                vn[e] = f16_bits_to_f32(hv);
+            }
+        }
+    }
     __syncthreads();
 
-    {
-        const int sub = lane % LP, slot = lane / LP;
-        for (int pi = wave * PPW + slot; pi - slot < n; pi += 4 * PPW) {
-            const bool act = pi < n;
-            uint4 kv = make_uint4(0, 0, 0, 0);
-            if (act) kv = *reinterpret_cast<const uint4*>(kc + (size_t)(p0 + pi) * kvd + kvh * HD + sub * 8);
-            const half2_t k01 = as_h2(kv.x), k23 = as_h2(kv.y), k45 = as_h2(kv.z), k67 = as_h2(kv.w);
+    // scores
+    for (int t0 = 0; t0 < n; t0 += TILE) {
+        const int pi = t0 + wave * PPW + slot;
+        const bool act = pi < n;
+        const int p = p0 + pi;
+        float kf[8];
+        if (act && p == pos) {
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float* qq = qs + g * HD + sub * 8;
-                float pd = qq[0] * (float)k01.x;
-                pd = pd + qq[1] * (float)k01.y;
-                pd = pd + qq[2] * (float)k23.x;
-                pd = pd + qq[3] * (float)k23.y;
-                pd = pd + qq[4] * (float)k45.x;
-                pd = pd + qq[5] * (float)k45.y;
-                pd = pd + qq[6] * (float)k67.x;
-                pd = pd + qq[7] * (float)k67.y;
-                pd = group_sum(pd, LP);
-                if (act && sub == 0) sc[g * chunk + pi] = pd * scale;
+            for (int e = 0; e < 8; e++) kf[e] = kn[sub * 8 + e];
+        } else {
+            uint4 kv = kpre;
+            if (t0 > 0) {
+                kv = make_uint4(0, 0, 0, 0);
+                if (act) kv = *reinterpret_cast<const uint4*>(a.kc + (size_t)p * kvd + kvh * HD + sub * 8);
             }
+            const half2_t k01 = as_h2(kv.x), k23 = as_h2(kv.y), k45 = as_h2(kv.z), k67 = as_h2(kv.w);
+            kf[0] = (float)k01.x; kf[1] = (float)k01.y; kf[2] = (float)k23.x; kf[3] = (float)k23.y;
+            kf[4] = (float)k45.x; kf[5] = (float)k45.y; kf[6] = (float)k67.x; kf[7] = (float)k67.y;
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float* qq = qs + g * HD + sub * 8;
+            float pd = qq[0] * kf[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) pd = pd + qq[e] * kf[e];
+            pd = group_sum(pd, LP);
+            if (act && sub == 0) sc[g * a.chunk_cap + pi] = pd * scale;
         }
     }
     __syncthreads();
 
     for (int g = wave; g < G; g += 4) {
         float m = -1e30f;
-        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * chunk + i]);
+        for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * a.chunk_cap + i]);
         m = wave_max(m);
         float l = 0.0f;
         for (int i = lane; i < n; i += 64) {
-            const float e = expf(sc[g * chunk + i] - m);
-            sc[g * chunk + i] = e;
+            const float e = expf(sc[g * a.chunk_cap + i] - m);
+            sc[g * a.chunk_cap + i] = e;
             l += e;
         }
         l = wave_sum(l);
-        if (lane == 0) { ml[2 * g] = m; ml[2 * g + 1] = l; }
+        if (lane == 0) {
+            ml[2 * g] = m;
+            ml[2 * g + 1] = l;
+        }
     }
     __syncthreads();
 
     // P.V: thread = (position group, 8-wide slice of the head dimension)
-    const int dsub = tid % LP, pg = tid / LP;
     float acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
     for (int pi = pg; pi < n; pi += PG) {
-        const uint4 vv = *reinterpret_cast<const uint4*>(vc + (size_t)(p0 + pi) * kvd + kvh * HD + dsub * 8);
-        const half2_t v01 = as_h2(vv.x), v23 = as_h2(vv.y), v45 = as_h2(vv.z), v67 = as_h2(vv.w);
-        const float vf[8] = {(float)v01.x, (float)v01.y, (float)v23.x, (float)v23.y,
-                             (float)v45.x, (float)v45.y, (float)v67.x, (float)v67.y};
+        const int p = p0 + pi;
+        float vf[8];
+        if (p == pos) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vf[e] = vn[dsub * 8 + e];
+        } else {
+            const uint4 vv = pi == pg ? vpre
+                                      : *reinterpret_cast<const uint4*>(a.vc + (size_t)p * kvd + kvh * HD + dsub * 8);
+            const half2_t v01 = as_h2(vv.x), v23 = as_h2(vv.y), v45 = as_h2(vv.z), v67 = as_h2(vv.w);
+            vf[0] = (float)v01.x; vf[1] = (float)v01.y; vf[2] = (float)v23.x; vf[3] = (float)v23.y;
+            vf[4] = (float)v45.x; vf[5] = (float)v45.y; vf[6] = (float)v67.x; vf[7] = (float)v67.y;
+        }
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float p = sc[g * chunk + pi];
+            const float pw = sc[g * a.chunk_cap + pi];
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] + vf[e] * p;
+            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] + vf[e] * pw;
         }
     }
-    __syncthreads();   // scores no longer needed: reuse smem for the cross-group sum
+    __syncthreads();   // scores no longer needed: smem is reused for the cross-group sum
     float* red = smem; // [PG][G][HD]
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 8; e++) red[(pg * G + g) * HD + dsub * 8 + e] = acc[g][e];
     __syncthreads();
-    float* out = part + ((size_t)kvh * max_splits + s) * G * (HD + 2);
+    float* out = a.part + ((size_t)kvh * a.max_splits + s) * G * (HD + 2);
     for (int i = tid; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
         float sum = 0.0f;
@@ -503,59 +642,56 @@ __global__ __launch_bounds__(256) void k_attn_split(const mdx_state* st, const f
         out[tid * (HD + 2) + HD] = ml[2 * tid];
         out[tid * (HD + 2) + HD + 1] = ml[2 * tid + 1];
     }
-}
 
-// Merges the split partials of one query head: grid = nq, block = HD.
-template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_combine(const mdx_state* st, const float* part,
-                                                      int max_splits, uint16_t* out16) {
-    const int L = st->pos + 1;
-    int splits, chunk;
-    split_plan(L, max_splits, splits, chunk);
-    const int h = blockIdx.x, kvh = h / G, g = h % G;
-    const int d = threadIdx.x;
-    const float* base = part + (size_t)kvh * max_splits * G * (HD + 2) + g * (HD + 2);
-    const size_t stride = (size_t)G * (HD + 2);
-    float m = -1e30f;
-    for (int s = 0; s < splits; s++) m = fmaxf(m, base[s * stride + HD]);
-    float l = 0.0f, o = 0.0f;
-    for (int s = 0; s < splits; s++) {
-        const float f = expf(base[s * stride + HD] - m);
-        l = l + base[s * stride + HD + 1] * f;
-        o = o + base[s * stride + d] * f;
-    }
-    out16[h * HD + d] = f32_to_f16_bits(o / l);
-}
-
-__global__ __launch_bounds__(256) void k_argmax_finish(mdx_state* st, const ArgPair* partial,
-                                                       int n, int* out_tokens, int advance) {
-    __shared__ ArgPair sh[256];
-    const int tid = threadIdx.x;
-    ArgPair b = {-INFINITY, -1};
-    for (int i = tid; i < n; i += 256) {
-        const ArgPair c = partial[i];
-        if (c.i >= 0 && (b.i < 0 || c.v > b.v)) b = c;   // i ascending: earlier wins ties
-    }
-    sh[tid] = b;
+    // the last block of this KV head merges all splits
+    __threadfence();
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) {
-            const ArgPair x = sh[tid], y = sh[tid + w];
-            ArgPair r = x;
-            if (y.i >= 0 && (x.i < 0 || y.v > x.v || (y.v == x.v && y.i < x.i))) r = y;
-            sh[tid] = r;
+    if (tid == 0) is_last = atomicAdd(&a.done[kvh], 1u) == (unsigned)(splits - 1);
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    const float* base = a.part + (size_t)kvh * a.max_splits * G * (HD + 2);
+    const size_t stride = (size_t)G * (HD + 2);
+    float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int gd = tid % GD4, sg = tid / GD4;
+    const int g = gd / (HD / 4), d4 = (gd % (HD / 4)) * 4;
+    if (sg < SG) {
+        for (int sp = sg; sp < splits; sp += SG) {
+            const float* ps = base + sp * stride + g * (HD + 2);
+            const float ms = ps[HD], ls = ps[HD + 1];
+            const float4 os = *reinterpret_cast<const float4*>(ps + d4);
+            const float mn = fmaxf(m, ms);
+            const float fa = expf(m - mn), fb = expf(ms - mn);
+            l = l * fa + ls * fb;
+            o[0] = o[0] * fa + os.x * fb;
+            o[1] = o[1] * fa + os.y * fb;
+            o[2] = o[2] * fa + os.z * fb;
+            o[3] = o[3] * fa + os.w * fb;
+            m = mn;
         }
-        __syncthreads();
     }
-    if (tid == 0) {
-        const int tok = sh[0].i < 0 ? 0 : sh[0].i;
-        st->argmax = tok;
-        st->token = tok;
-        st->mode = 0;
-        if (out_tokens) out_tokens[st->n_out] = tok;
-        if (out_tokens) st->n_out = st->n_out + 1;
-        st->pos = st->pos + advance;
+    __syncthreads();
+    float* mr = smem;                       // [SG][GD4][6]
+    if (sg < SG) {
+        float* r = mr + (sg * GD4 + gd) * 6;
+        r[0] = m; r[1] = l; r[2] = o[0]; r[3] = o[1]; r[4] = o[2]; r[5] = o[3];
     }
+    __syncthreads();
+    if (sg == 0) {
+        float M = -INFINITY;
+        for (int k = 0; k < SG; k++) M = fmaxf(M, mr[(k * GD4 + gd) * 6]);
+        float Ls = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < SG; k++) {
+            const float* r = mr + (k * GD4 + gd) * 6;
+            if (r[0] == -INFINITY) continue;
+            const float f = expf(r[0] - M);
+            Ls = Ls + r[1] * f;
+            for (int e = 0; e < 4; e++) O[e] = O[e] + r[2 + e] * f;
+        }
+        uint16_t* dst = a.out16 + (size_t)(kvh * G + g) * HD + d4;
+        for (int e = 0; e < 4; e++) dst[e] = f32_to_f16_bits(O[e] / Ls);
+    }
+    if (tid == 0) atomicExch(&a.done[kvh], 0u);
 }
 
 __global__ void k_advance(mdx_state* st, int advance) {
@@ -566,21 +702,9 @@ __global__ void k_advance(mdx_state* st, int advance) {
 
 extern "C" {
 
-int mdx_launch_embed(const mdx_state* state, const float* emb_table, const float* emb_in,
-                     float* hidden, int d, int vocab, void* stream) {
-    const int blocks = (d + 255) / 256;
-    hipLaunchKernelGGL(k_embed, dim3(blocks), dim3(256), 0, (hipStream_t)stream, state, emb_table,
-                       emb_in, hidden, d, vocab);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
 int mdx_launch_norm_gemv(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
                          int epilogue, void* out, void* stream) {
-    GemvArgs a = {};
-    a.w = (const uint8_t*)w->w;
-    a.scale = w->scale;
-    a.K = w->K;
-    a.N = w->N;
+    GemvArgs a = base_args(w);
     a.xmode = XM_NORM;
     a.xf32 = hidden;
     a.norm_w = norm_w;
@@ -592,96 +716,83 @@ int mdx_launch_norm_gemv(const float* hidden, const float* norm_w, float eps, co
         a.epi = EP_SWIGLU;
         a.out_f16 = (uint16_t*)out;
     } else {
-        a.n_units = w->N;
-        a.unit_rows = 1;
         a.epi = EP_STORE;
         a.out_f32 = (float*)out;
     }
     const int kind = kind_from(w, 0);
-    int rw = rows_per_wave_for(kind, a.n_units * a.unit_rows, a.K);
+    int rw = rows_per_wave_for(a.n_units * a.unit_rows);
     if (a.unit_rows == 2 && rw < 2) rw = 2;
-    return launch_gemv(kind, a, rw, stream);
+    return launch_gemv(kind, a, rw, 0, stream);
+}
+
+int mdx_launch_embed_norm_gemv(const mdx_state* state, const float* emb_table, const float* emb_in,
+                               int vocab, float* hidden, const float* norm_w, float eps,
+                               const mdx_wdesc* w, float* out, void* stream) {
+    GemvArgs a = base_args(w);
+    a.xmode = XM_EMBED;
+    a.st_in = state;
+    a.emb_table = emb_table;
+    a.xf32 = emb_in;
+    a.vocab = vocab;
+    a.hidden_out = hidden;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.epi = EP_STORE;
+    a.out_f32 = out;
+    const int kind = kind_from(w, 0);
+    return launch_gemv(kind, a, rows_per_wave_for(w->N), 0, stream);
 }
 
 int mdx_launch_gemv_add(const uint16_t* x16, const mdx_wdesc* w, float* out, void* stream) {
-    GemvArgs a = {};
-    a.w = (const uint8_t*)w->w;
-    a.scale = w->scale;
-    a.K = w->K;
-    a.N = w->N;
-    a.n_units = w->N;
-    a.unit_rows = 1;
+    GemvArgs a = base_args(w);
     a.xmode = XM_F16;
     a.x16 = x16;
     a.epi = EP_ADD;
     a.out_f32 = out;
     const int kind = kind_from(w, 0);
-    return launch_gemv(kind, a, rows_per_wave_for(kind, a.N, a.K), stream);
+    return launch_gemv(kind, a, rows_per_wave_for(a.N), 0, stream);
 }
 
 int mdx_launch_gemv_f16in(const uint16_t* x16, const mdx_wdesc* w, float* y, void* stream) {
-    GemvArgs a = {};
-    a.w = (const uint8_t*)w->w;
-    a.scale = w->scale;
-    a.K = w->K;
-    a.N = w->N;
-    a.n_units = w->N;
-    a.unit_rows = 1;
+    GemvArgs a = base_args(w);
     a.xmode = XM_F16;
     a.x16 = x16;
     a.epi = EP_STORE;
     a.out_f32 = y;
     const int kind = kind_from(w, 0);
-    return launch_gemv(kind, a, rows_per_wave_for(kind, a.N, a.K), stream);
+    return launch_gemv(kind, a, rows_per_wave_for(a.N), 0, stream);
 }
 
 int mdx_launch_gemv(const float* x, const mdx_wdesc* w, int x_fp32_exact, float* y, void* stream) {
-    GemvArgs a = {};
-    a.w = (const uint8_t*)w->w;
-    a.scale = w->scale;
-    a.K = w->K;
-    a.N = w->N;
-    a.n_units = w->N;
-    a.unit_rows = 1;
+    GemvArgs a = base_args(w);
     a.xmode = XM_F32;
     a.xf32 = x;
     a.epi = EP_STORE;
     a.out_f32 = y;
     const int kind = kind_from(w, x_fp32_exact);
-    return launch_gemv(kind, a, rows_per_wave_for(kind, a.N, a.K), stream);
+    return launch_gemv(kind, a, rows_per_wave_for(a.N), 0, stream);
 }
 
-int mdx_lmhead_partials(int N) {
-    const int rw = rows_per_wave_for(KI8, N, 0);
-    return (N + 4 * rw - 1) / (4 * rw);
-}
+size_t mdx_lmhead_scratch_bytes(void) { return 16; }
 
 int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
-                      float* logits, void* partial, void* stream) {
-    GemvArgs a = {};
-    a.w = (const uint8_t*)w->w;
-    a.scale = w->scale;
-    a.K = w->K;
-    a.N = w->N;
-    a.n_units = w->N;
-    a.unit_rows = 1;
+                      float* logits, void* scratch, mdx_state* state, int* out_tokens, int advance,
+                      void* stream) {
+    GemvArgs a = base_args(w);
     a.xmode = XM_NORM;
     a.xf32 = hidden;
     a.norm_w = norm_w;
     a.eps = eps;
     a.epi = EP_LOGITS;
     a.out_f32 = logits;
-    a.partial = (ArgPair*)partial;
+    a.amax_key = (unsigned long long*)scratch;
+    a.done = (unsigned int*)((char*)scratch + 8);
+    a.st = state;
+    a.out_tokens = out_tokens;
+    a.advance = advance;
     // fp16 rows take fp32 activations here (the reference's CPU lm_head)
     const int kind = kind_from(w, 1);
-    return launch_gemv(kind, a, rows_per_wave_for(KI8, w->N, 0), stream);
-}
-
-int mdx_launch_argmax_finish(mdx_state* state, const void* partial, int n_partials,
-                             int* out_tokens, int advance, void* stream) {
-    hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(256), 0, (hipStream_t)stream, state,
-                       (const ArgPair*)partial, n_partials, out_tokens, advance);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    return launch_gemv(kind, a, rows_per_wave_for(w->N), 1024, stream);
 }
 
 int mdx_launch_advance(mdx_state* state, int advance, void* stream) {
@@ -689,44 +800,53 @@ int mdx_launch_advance(mdx_state* state, int advance, void* stream) {
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int mdx_launch_qk_rope_append(const mdx_state* state, const float* qkv, const float* q_norm,
-                              const float* k_norm, float eps, const float* cos_t,
-                              const float* sin_t, int nq, int nkv, int hd, int rope_style,
-                              float* q_out, uint16_t* k_cache, uint16_t* v_cache, void* stream) {
-    if (hd % 2) return -1;
-    hipLaunchKernelGGL(k_qk_rope_append, dim3(nq + 2 * nkv), dim3(64), 0, (hipStream_t)stream,
-                       state, qkv, q_norm, k_norm, eps, cos_t, sin_t, nq, nkv, hd, rope_style,
-                       q_out, k_cache, v_cache);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+int mdx_attn_max_splits(int max_seq) {
+    (void)max_seq;
+    return 64;
 }
 
-size_t mdx_attn_decode_scratch_floats(int nq, int hd, int max_splits) {
-    return (size_t)nq * max_splits * (hd + 2);
+size_t mdx_attn_decode_scratch_bytes(int nq, int nkv, int hd, int max_splits) {
+    return (size_t)nq * max_splits * (hd + 2) * 4 + (size_t)nkv * 4;
 }
 
-int mdx_launch_attn_decode(const mdx_state* state, const float* q, const uint16_t* k_cache,
-                           const uint16_t* v_cache, int nq, int nkv, int hd, int max_seq,
-                           int max_splits, float* part, uint16_t* attn_out16, void* stream) {
-    if (nkv <= 0 || nq % nkv) return -1;
+int mdx_launch_attn_decode(const mdx_state* state, const float* qkv, const float* q_norm,
+                           const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                           int rope_style, int nq, int nkv, int hd, int max_seq, int max_splits,
+                           uint16_t* k_cache, uint16_t* v_cache, void* scratch, uint16_t* attn_out16,
+                           void* stream) {
+    if (nkv <= 0 || nq % nkv || max_splits <= 0 || hd % 8) return -1;
     const int G = nq / nkv;
-    // The split plan keeps chunk <= 16 positions as long as L <= 16*max_splits;
-    // L <= max_seq, so that bound is required here (it sizes the LDS score row).
-    if ((long)max_splits * 16 < (long)max_seq) return -1;
-    const int chunk_max = 16;
+    AttnArgs a;
+    a.st = state;
+    a.qkv = qkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.eps = eps;
+    a.cos_t = cos_t;
+    a.sin_t = sin_t;
+    a.style = rope_style;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.nkv = nkv;
+    a.max_splits = max_splits;
+    a.chunk_cap = (max_seq + max_splits - 1) / max_splits;
+    if (a.chunk_cap < 16) a.chunk_cap = 16;
+    a.part = (float*)scratch;
+    a.done = (unsigned int*)((char*)scratch + (size_t)nq * max_splits * (hd + 2) * 4);
+    a.out16 = attn_out16;
     const int LP = hd / 8;
-    const int PG = 256 / (LP > 0 ? LP : 1);
-    size_t lds_a = (size_t)(G * hd + G * chunk_max) * 4;
-    size_t lds_b = (size_t)PG * G * hd * 4;
-    const size_t lds = lds_a > lds_b ? lds_a : lds_b;
+    const int PG = 256 / LP;
+    const size_t lds_a = (size_t)(G * hd + 2 * hd + G * a.chunk_cap) * 4;
+    const size_t lds_b = (size_t)PG * G * hd * 4;
+    const size_t lds_c = (size_t)256 * 6 * 4;
+    size_t lds = lds_a > lds_b ? lds_a : lds_b;
+    if (lds_c > lds) lds = lds_c;
     if (lds > 64 * 1024) return -5;
     dim3 grid(nkv, max_splits);
-#define MDX_ATTN(HD_, G_)                                                                        \
-    if (hd == HD_ && G == G_) {                                                                  \
-        hipLaunchKernelGGL((k_attn_split<HD_, G_>), grid, dim3(256), lds, (hipStream_t)stream,   \
-                           state, q, k_cache, v_cache, nkv, max_splits, part);                   \
-        hipLaunchKernelGGL((k_attn_combine<HD_, G_>), dim3(nq), dim3(HD_), 0,                   \
-                           (hipStream_t)stream, state, part, max_splits, attn_out16);            \
-        return hipGetLastError() == hipSuccess ? 0 : -4;                                         \
+#define MDX_ATTN(HD_, G_)                                                                          \
+    if (hd == HD_ && G == G_) {                                                                    \
+        hipLaunchKernelGGL((k_attn_decode<HD_, G_>), grid, dim3(256), lds, (hipStream_t)stream, a); \
+        return hipGetLastError() == hipSuccess ? 0 : -4;                                           \
     }
     MDX_ATTN(64, 1) MDX_ATTN(64, 2) MDX_ATTN(64, 4) MDX_ATTN(64, 8)
     MDX_ATTN(128, 1) MDX_ATTN(128, 2) MDX_ATTN(128, 4) MDX_ATTN(128, 8)

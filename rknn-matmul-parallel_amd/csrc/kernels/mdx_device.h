@@ -70,15 +70,18 @@ int mdxrt_fill_u32(void* dst, uint32_t value, size_t n, void* stream);
 
 /* ---- decode (M = 1) kernels ---- */
 
-/* hidden[d] fp32 <- embeddings[state->token] or emb_in, per state->mode. */
-int mdx_launch_embed(const mdx_state* state, const float* emb_table, const float* emb_in,
-                     float* hidden, int d, int vocab, void* stream);
-
 /* Fused RMSNorm + projection: x16 = fp16((hidden*rms)*norm_w), y = x16 . W^T
  * (x scale).  epilogue: 0 store y fp32, 1 SwiGLU over rows [0,N/2) and
  * [N/2,N) writing act fp16 [N/2]. */
 int mdx_launch_norm_gemv(const float* hidden, const float* norm_w, float eps,
                          const mdx_wdesc* w, int epilogue, void* out, void* stream);
+
+/* First projection of a step: the input row is embeddings[state->token]
+ * (state->mode 0) or emb_in (mode 1); it is copied to hidden[d] and then
+ * RMSNorm + projection as mdx_launch_norm_gemv, storing y fp32. */
+int mdx_launch_embed_norm_gemv(const mdx_state* state, const float* emb_table, const float* emb_in,
+                               int vocab, float* hidden, const float* norm_w, float eps,
+                               const mdx_wdesc* w, float* out, void* stream);
 
 /* y = fp16 x . W^T (x scale); out[n] += y[n] (residual add, fp32). */
 int mdx_launch_gemv_add(const uint16_t* x16, const mdx_wdesc* w, float* out, void* stream);
@@ -92,36 +95,32 @@ int mdx_launch_gemv_f16in(const uint16_t* x16, const mdx_wdesc* w, float* y, voi
 int mdx_launch_gemv(const float* x, const mdx_wdesc* w, int x_fp32_exact, float* y,
                     void* stream);
 
-/* Per-head QK-norm + RoPE of q,k from the merged QKV output (fp32
- * [q|k|v]); q written fp32 [nq*hd]; k,v appended as fp16 at row state->pos
- * of the layer cache [max_seq][nkv*hd].  q_norm/k_norm may be NULL. */
-int mdx_launch_qk_rope_append(const mdx_state* state, const float* qkv, const float* q_norm,
-                              const float* k_norm, float eps, const float* cos_t,
-                              const float* sin_t, int nq, int nkv, int hd, int rope_style,
-                              float* q_out, uint16_t* k_cache, uint16_t* v_cache, void* stream);
+/* One decode attention layer: QK-norm (q_norm/k_norm may be NULL) + RoPE at
+ * row state->pos of the tables, append of the new K/V (fp16) at that row
+ * of the layer cache [max_seq][nkv*hd], split-K GQA attention over rows
+ * [0, state->pos] and the merge of the splits; writes the fp16 attention
+ * output [nq*hd].  qkv is the fp32 [q|k|v] projection output.  scratch:
+ * mdx_attn_decode_scratch_bytes() bytes whose last nkv words are zero
+ * between launches (the kernel leaves them zero). */
+int mdx_attn_max_splits(int max_seq);
+size_t mdx_attn_decode_scratch_bytes(int nq, int nkv, int hd, int max_splits);
+int mdx_launch_attn_decode(const mdx_state* state, const float* qkv, const float* q_norm,
+                           const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                           int rope_style, int nq, int nkv, int hd, int max_seq, int max_splits,
+                           uint16_t* k_cache, uint16_t* v_cache, void* scratch, uint16_t* attn_out16,
+                           void* stream);
 
-/* Split-K GQA decode attention over cache rows [0, state->pos]; writes the
- * fp16 attention output [nq*hd].  part is scratch of
- * mdx_attn_decode_scratch_floats(nq, hd, max_splits) floats; max_splits must
- * be >= ceil(max_seq / 16). */
-size_t mdx_attn_decode_scratch_floats(int nq, int hd, int max_splits);
-int mdx_launch_attn_decode(const mdx_state* state, const float* q, const uint16_t* k_cache,
-                           const uint16_t* v_cache, int nq, int nkv, int hd, int max_seq,
-                           int max_splits, float* part, uint16_t* attn_out16, void* stream);
-
-/* Final RMSNorm + INT8 (or fp16/fp32-row) lm_head writing logits fp32 [N]
- * and per-block (value,index) partials; then the argmax reduction.
- * lm_kind: MDX_W_I8 (fp16 activations, the NPU path), MDX_W_F16 with fp32
- * activations (the CPU fp16 GEMV), MDX_W_F32 (fp32 rows).
- * partial holds mdx_lmhead_partials(N) pairs of 8 bytes. */
-int mdx_lmhead_partials(int N);
-int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
-                      float* logits, void* partial, void* stream);
-/* Reduces the partials to the argmax (lowest index on ties), stores it in
+/* Final RMSNorm + lm_head writing logits fp32 [N], with the argmax (lowest
+ * index on ties) fused: the last block to finish stores it in
  * state->argmax and state->token, appends it to out_tokens[state->n_out++]
- * when out_tokens != NULL, and advances state->pos by `advance`. */
-int mdx_launch_argmax_finish(mdx_state* state, const void* partial, int n_partials,
-                             int* out_tokens, int advance, void* stream);
+ * when out_tokens != NULL and advances state->pos by `advance`.
+ * w->kind: MDX_W_I8 (fp16 activations, the NPU path), MDX_W_F16 with fp32
+ * activations (the CPU fp16 GEMV), MDX_W_F32 (fp32 rows).  scratch:
+ * mdx_lmhead_scratch_bytes() zero bytes (left zero by the kernel). */
+size_t mdx_lmhead_scratch_bytes(void);
+int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
+                      float* logits, void* scratch, mdx_state* state, int* out_tokens, int advance,
+                      void* stream);
 /* state->pos += advance (prefill-mode steps). */
 int mdx_launch_advance(mdx_state* state, int advance, void* stream);
 

@@ -117,25 +117,43 @@ int mdxrt_graph_begin(void* stream) {
     return 0;
 }
 
-int mdxrt_graph_end(void* stream, void** exec) {
+// A captured graph and its executable instance.  The graph is kept alive as
+// long as the instance: the runtime (and tools that trace graph launches) may
+// refer to the graph's nodes when the instance is launched.
+struct mdx_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+int mdxrt_graph_end(void* stream, void** handle) {
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
-    *exec = nullptr;
+    *handle = nullptr;
     MDX_CHECK(hipStreamEndCapture((hipStream_t)stream, &g), "hipStreamEndCapture");
     hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return fail(e, "hipGraphInstantiate");
-    *exec = (void*)ge;
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(e, "hipGraphInstantiate");
+    }
+    mdx_graph* h = new mdx_graph{g, ge};
+    *handle = (void*)h;
     return 0;
 }
 
-int mdxrt_graph_launch(void* exec, void* stream) {
-    MDX_CHECK(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)stream), "hipGraphLaunch");
+int mdxrt_graph_launch(void* handle, void* stream) {
+    MDX_CHECK(hipGraphLaunch(static_cast<mdx_graph*>(handle)->exec, (hipStream_t)stream),
+              "hipGraphLaunch");
     return 0;
 }
 
-int mdxrt_graph_destroy(void* exec) {
-    if (exec) MDX_CHECK(hipGraphExecDestroy((hipGraphExec_t)exec), "hipGraphExecDestroy");
+int mdxrt_graph_destroy(void* handle) {
+    if (!handle) return 0;
+    mdx_graph* h = static_cast<mdx_graph*>(handle);
+    hipError_t e1 = hipGraphExecDestroy(h->exec);
+    hipError_t e2 = hipGraphDestroy(h->graph);
+    delete h;
+    if (e1 != hipSuccess) return fail(e1, "hipGraphExecDestroy");
+    if (e2 != hipSuccess) return fail(e2, "hipGraphDestroy");
     return 0;
 }
 

@@ -115,7 +115,8 @@ def lib() -> C.CDLL:
             "mdx_time_prefill": (C.c_int, [P, _F, C.c_int, C.c_int, _F]),
             "mdx_debug_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
-            "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _F, _U16, _U16, _F]),
+            "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                                C.c_float, _F, _F, _F, _U16, _U16, _F, _U16, _U16]),
             "mdx_debug_attn_prefill": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _F, _U16,
                                                  _U16, _F]),
             "mdx_debug_qk_rope": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
@@ -218,14 +219,19 @@ def gemm(kind: int, M: int, K: int, N: int, w: np.ndarray, scales, x) -> np.ndar
     return y.reshape(M, N)
 
 
-def attn_decode(nq, nkv, hd, L, q, k16, v16) -> np.ndarray:
-    q = _f32(q)
-    k16 = np.ascontiguousarray(k16, np.uint16)
-    v16 = np.ascontiguousarray(v16, np.uint16)
+def attn_decode(nq, nkv, hd, pos, style, theta, eps, q_norm, k_norm, qkv, k16, v16):
+    """Fused decode attention at position pos; returns (out fp32, k_new16, v_new16)."""
+    qkv = _f32(qkv)
+    qn, kn = _f32(q_norm), _f32(k_norm)
+    k16 = np.ascontiguousarray(k16, np.uint16) if pos > 0 else None
+    v16 = np.ascontiguousarray(v16, np.uint16) if pos > 0 else None
     out = np.empty(nq * hd, np.float32)
-    _check(lib().mdx_debug_attn_decode(nq, nkv, hd, L, _p(q, _F), _p(k16, _U16), _p(v16, _U16),
-                                       _p(out, _F)), "attn_decode")
-    return out
+    kn16 = np.empty(nkv * hd, np.uint16)
+    vn16 = np.empty(nkv * hd, np.uint16)
+    _check(lib().mdx_debug_attn_decode(nq, nkv, hd, pos, style, theta, eps, _p(qn, _F), _p(kn, _F),
+                                       _p(qkv, _F), _p(k16, _U16), _p(v16, _U16), _p(out, _F),
+                                       _p(kn16, _U16), _p(vn16, _U16)), "attn_decode")
+    return out, kn16, vn16
 
 
 def attn_prefill(nq, nkv, hd, S, M, q, k16, v16) -> np.ndarray:

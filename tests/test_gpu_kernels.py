@@ -128,18 +128,35 @@ def _kv(rng, L, kvd):
     return k, v
 
 
-@pytest.mark.parametrize("L", [1, 2, 17, 513, 576, 4097])
-def test_attention_decode(mdx, gpu, oracle_lib, L):
-    rng = np.random.default_rng(L)
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("pos", [0, 1, 16, 17, 512, 575, 1023, 4096])
+def test_attention_decode_fused(mdx, gpu, oracle_lib, pos, style):
+    """QK-norm + RoPE + K/V append + split-K GQA attention + merge, one kernel."""
+    rng = np.random.default_rng(pos * 2 + style)
     nq, nkv, hd = 16, 8, 128
-    q = rng.standard_normal(nq * hd).astype(np.float32)
-    k, v = _kv(rng, L, nkv * hd)
-    out = mdx.attn_decode(nq, nkv, hd, L, q, k.view(np.uint16), v.view(np.uint16))
-    ref = oracle_lib.attention(q, k.astype(np.float32), v.astype(np.float32), nq, nkv, hd, L)
-    ref16 = ref.astype(np.float16).astype(np.float32)
-    assert rel_err(out, ref16) < TOL
-    if L == 1:
-        assert np.array_equal(out, np.repeat(v.astype(np.float32).reshape(nkv, hd), 2, axis=0).ravel())
+    qd, kvd = nq * hd, nkv * hd
+    qkv = (rng.standard_normal(qd + 2 * kvd) * 2).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    k, v = _kv(rng, pos, kvd)
+    out, k_new, v_new = mdx.attn_decode(nq, nkv, hd, pos, style, 1e6, 1e-6, qn, kn, qkv,
+                                        k.view(np.uint16), v.view(np.uint16))
+    c, s = oracle_lib.rope_tables(pos + 1, hd, 1e6)
+    q = np.concatenate([oracle_lib.rms_norm(qkv[h * hd:(h + 1) * hd], qn, 1e-6) for h in range(nq)])
+    kr = np.concatenate([oracle_lib.rms_norm(qkv[qd + h * hd:qd + (h + 1) * hd], kn, 1e-6)
+                         for h in range(nkv)])
+    q = oracle_lib.apply_rope(q, c[pos], s[pos], nq, hd, style)
+    kr = oracle_lib.apply_rope(kr, c[pos], s[pos], nkv, hd, style)
+    k16 = kr.astype(np.float16)
+    v16 = qkv[qd + kvd:].astype(np.float16)
+    assert rel_err(k_new.view(np.float16).astype(np.float32), k16.astype(np.float32)) < 1e-3
+    assert np.array_equal(v_new, v16.view(np.uint16))
+    kc = np.concatenate([k.astype(np.float32), k_new.view(np.float16).astype(np.float32)])
+    vc = np.concatenate([v.astype(np.float32), v16.astype(np.float32)])
+    ref = oracle_lib.attention(q, kc, vc, nq, nkv, hd, pos + 1)
+    assert rel_err(out, ref.astype(np.float16).astype(np.float32)) < TOL
+    if pos == 0:
+        assert np.array_equal(out, np.repeat(v16.astype(np.float32).reshape(nkv, hd), 2, axis=0).ravel())
 
 
 @pytest.mark.parametrize("S,M", [(0, 60), (0, 1), (100, 33), (4000, 64)])
