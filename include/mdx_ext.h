@@ -32,6 +32,12 @@ int mdx_device_count(void);
 /* Last HIP runtime message recorded by the library (thread-local). */
 const char* mdx_last_error(void);
 
+/* Decode path of a context: 1 when a step is one cooperative launch of the
+ * whole model (the 0.6B shape with one weight kind and the INT8 lm_head;
+ * MDX_PERSIST=0 in the environment at creation turns it off), 0 when it is
+ * the per-stage kernel sequence. */
+int mdx_decode_path(const MatmulDecoderContext* ctx);
+
 /* matmul_decoder_step with the lm_head and argmax but without copying the
  * logits to the host (the pybind step_get_token path). */
 int mdx_step_token(MatmulDecoderContext* ctx, int token_id, const float* embedding);

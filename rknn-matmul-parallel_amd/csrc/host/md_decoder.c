@@ -63,6 +63,9 @@ struct MatmulDecoderContext {
     int pgraph_next;
     int capture_M;
     int use_graphs;          /* 0 when MDX_GRAPHS=0: same kernels, launched one by one */
+    int persist;             /* 1: decode steps run as one cooperative launch */
+    void* d_xbuf;            /* exchange words of the persistent step */
+    mdx_persist_args pargs;
     mdx_state* h_state;
     float* h_io;
     size_t h_io_floats;
@@ -353,6 +356,7 @@ static int layout(MatmulDecoderContext* c, const md_source* s) {
     CARVE(c->d_attn16, (size_t)c->qd * 2);
     CARVE(c->d_act16, (size_t)c->F * 2);
     CARVE(c->d_partial, mdx_lmhead_scratch_bytes());
+    CARVE(c->d_xbuf, mdx_persist_xbuf_bytes());
     const int mm = c->max_m;
     const int kmax = c->F > c->qd ? (c->F > c->d ? c->F : c->d) : (c->qd > c->d ? c->qd : c->d);
     CARVE(c->d_bhidden, (size_t)mm * c->d * 4);
@@ -606,6 +610,91 @@ static void* prefill_graph(MatmulDecoderContext* c, int M) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* Persistent step                                                           */
+/* ------------------------------------------------------------------------ */
+
+static int at_stride(const void* p0, const void* pl, int l, long long stride) {
+    if (!p0 || !pl) return p0 == pl;
+    return (const char*)pl - (const char*)p0 == (long long)l * stride;
+}
+
+/* The whole step becomes one cooperative launch when the model has the shape
+ * that kernel is built for, one weight kind throughout, the INT8 lm_head,
+ * and layers laid out at a constant stride in the arena (always true for the
+ * arena layout, checked anyway).  MDX_PERSIST=0 keeps the per-kernel path. */
+static void setup_persist(MatmulDecoderContext* c) {
+    c->persist = 0;
+    const char* e = getenv("MDX_PERSIST");
+    if (e && e[0] == '0') return;
+    if (c->n_lm > 1 || c->config.disable_npu_lm_head || c->L < 1 || c->V < 256) return;
+    if (!mdx_persist_shape_ok(c->d, c->nq, c->nkv, c->hd, c->F)) return;
+    const md_layer* l0 = &c->layers[0];
+    const int kind = l0->qkv.kind;
+    if (kind != MDX_W_F16 && kind != MDX_W_I8 && kind != MDX_W_I4) return;
+    const long long stride = c->L > 1 ? (const char*)c->layers[1].qkv.w - (const char*)l0->qkv.w : 0;
+    for (int l = 0; l < c->L; l++) {
+        const md_layer* ly = &c->layers[l];
+        if (ly->qkv.kind != kind || ly->o.kind != kind || ly->gu.kind != kind || ly->down.kind != kind)
+            return;
+        if (!at_stride(l0->qkv.w, ly->qkv.w, l, stride) || !at_stride(l0->qkv.scale, ly->qkv.scale, l, stride) ||
+            !at_stride(l0->o.w, ly->o.w, l, stride) || !at_stride(l0->o.scale, ly->o.scale, l, stride) ||
+            !at_stride(l0->gu.w, ly->gu.w, l, stride) || !at_stride(l0->gu.scale, ly->gu.scale, l, stride) ||
+            !at_stride(l0->down.w, ly->down.w, l, stride) ||
+            !at_stride(l0->down.scale, ly->down.scale, l, stride) ||
+            !at_stride(l0->in_norm, ly->in_norm, l, stride) ||
+            !at_stride(l0->post_norm, ly->post_norm, l, stride) ||
+            !at_stride(l0->q_norm, ly->q_norm, l, stride) || !at_stride(l0->k_norm, ly->k_norm, l, stride) ||
+            ly->kc != l0->kc + (size_t)l * c->max_seq * c->kvd ||
+            ly->vc != l0->vc + (size_t)l * c->max_seq * c->kvd)
+            return;
+    }
+    if (!mdx_persist_usable(kind)) return;
+    mdx_persist_args* a = &c->pargs;
+    memset(a, 0, sizeof *a);
+    a->kind = kind;
+    a->n_layers = c->L;
+    a->vocab = c->V;
+    a->max_seq = c->max_seq;
+    a->rope_style = c->config.rope_style;
+    a->eps = c->config.rms_eps;
+    a->state = c->d_state;
+    a->l0.wqkv = l0->qkv.w;
+    a->l0.sqkv = l0->qkv.scale;
+    a->l0.wo = l0->o.w;
+    a->l0.so = l0->o.scale;
+    a->l0.wgu = l0->gu.w;
+    a->l0.sgu = l0->gu.scale;
+    a->l0.wdown = l0->down.w;
+    a->l0.sdown = l0->down.scale;
+    a->l0.in_norm = l0->in_norm;
+    a->l0.post_norm = l0->post_norm;
+    a->l0.q_norm = l0->q_norm;
+    a->l0.k_norm = l0->k_norm;
+    a->l0.kc = l0->kc;
+    a->l0.vc = l0->vc;
+    a->layer_stride = stride;
+    a->kv_stride = (long long)c->max_seq * c->kvd;
+    a->emb_table = c->d_emb;
+    a->emb_in = c->d_emb_in;
+    a->cos_t = c->d_cos;
+    a->sin_t = c->d_sin;
+    a->final_norm = c->d_final_norm;
+    a->lm_w = (const int8_t*)c->lm.w;
+    a->lm_scale = c->lm.scale;
+    a->logits = c->d_logits;
+    a->hidden_out = c->d_hidden;
+    a->xbuf = c->d_xbuf;
+    c->persist = 1;
+}
+
+static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
+    c->pargs.head = head;
+    c->pargs.advance = 1;
+    c->pargs.out_tokens = out_tokens;
+    return mdx_launch_persist_step(&c->pargs, c->stream);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Create / destroy                                                          */
 /* ------------------------------------------------------------------------ */
 
@@ -740,6 +829,10 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     if ((size_t)c->max_m * c->d > c->h_io_floats) c->h_io_floats = (size_t)c->max_m * c->d;
     if (mdxrt_host_alloc((void**)&c->h_io, c->h_io_floats * 4)) goto fail;
     memset(c->h_state, 0, sizeof(mdx_state));
+    setup_persist(c);
+    if (md_verbose())
+        printf("[MatmulDecoder] decode step: %s\n",
+               c->persist ? "one cooperative launch" : "per-stage kernels");
     return c;
 fail:
     fprintf(stderr, "[MatmulDecoder] create failed%s%s\n", mdxrt_last_error()[0] ? ": " : "",
@@ -872,15 +965,24 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     }
     rc = set_state(c, token_id, embedding);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
-    if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
-    if (!rc) rc = launch_seq(c, want_head ? c->g_head : c->g_adv, want_head ? seq_head : seq_adv);
+    if (c->persist) {
+        if (!rc) rc = launch_persist(c, want_head, NULL);
+        if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
+    } else {
+        if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
+        if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
+        if (!rc) rc = launch_seq(c, want_head ? c->g_head : c->g_adv, want_head ? seq_head : seq_adv);
+    }
     if (!rc) rc = mdxrt_event_record(c->ev2, c->stream);
     if (!rc && output_logits) rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
     if (rc) {
         fprintf(stderr, "[MatmulDecoder] step failed: %s\n", mdxrt_last_error());
+        return MATMUL_DECODER_ERR_RKNN;
+    }
+    if (c->h_state->pad[1]) {
+        fprintf(stderr, "[MatmulDecoder] step failed: a workgroup timed out waiting for another\n");
         return MATMUL_DECODER_ERR_RKNN;
     }
     float layers_ms = 0.0f, head_ms = 0.0f;
@@ -895,7 +997,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     c->stats.matmul_ms = layers_ms;
     c->stats.rebind_ms = 0.0f;
     c->stats.cpu_ops_ms = 0.0f;
-    c->stats.lm_head_ms = want_head ? head_ms : 0.0f;
+    c->stats.lm_head_ms = want_head ? head_ms : 0.0f;   /* 0 for the one-launch step (inside matmul_ms) */
     c->stats.convert_ms = total - layers_ms - (want_head ? head_ms : 0.0f);
     if (c->stats.convert_ms < 0) c->stats.convert_ms = 0;
     c->stats.n_steps++;
@@ -1101,18 +1203,24 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
         if (mdxrt_malloc((void**)&c->d_tokens, (size_t)cap * 4)) return MATMUL_DECODER_ERR_MEMORY;
         c->tokens_cap = cap;
     }
-    if (c->use_graphs && !c->g_greedy && capture(c, seq_greedy, &c->g_greedy))
+    if (!c->persist && c->use_graphs && !c->g_greedy && capture(c, seq_greedy, &c->g_greedy))
         return MATMUL_DECODER_ERR_RKNN;
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
     c->h_state->token = first_token;
     int rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    for (int i = 0; i < n_steps && !rc; i++) rc = launch_seq(c, c->g_greedy, seq_greedy);
+    for (int i = 0; i < n_steps && !rc; i++)
+        rc = c->persist ? launch_persist(c, 1, c->d_tokens) : launch_seq(c, c->g_greedy, seq_greedy);
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
+    if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
     if (!rc) rc = mdxrt_d2h(out_tokens, c->d_tokens, (size_t)n_steps * 4);
     if (rc) return MATMUL_DECODER_ERR_RKNN;
+    if (c->h_state->pad[1]) {
+        fprintf(stderr, "[MatmulDecoder] generate failed: a workgroup timed out waiting for another\n");
+        return MATMUL_DECODER_ERR_RKNN;
+    }
     if (device_ms) mdxrt_event_elapsed_ms(c->ev0, c->ev1, device_ms);
     c->seq_len += n_steps;
     return 0;
@@ -1189,4 +1297,9 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
 
 const char* mdx_version(void) { return "1.0.0 gfx950"; }
 int mdx_device_count(void) { return mdxrt_device_count(); }
+
+int mdx_decode_path(const MatmulDecoderContext* c) {
+    if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
+    return c->persist ? 1 : 0;
+}
 const char* mdx_last_error(void) { return mdxrt_last_error(); }

@@ -124,6 +124,57 @@ int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const
 /* state->pos += advance (prefill-mode steps). */
 int mdx_launch_advance(mdx_state* state, int advance, void* stream);
 
+/* ---- whole decode step in one cooperative launch (mdx_persist.hip) ---- */
+
+/* Per-layer device pointers of the persistent step (all projections of one
+ * kind, W^T rows as above; scales may be NULL; q_norm/k_norm may be NULL). */
+typedef struct {
+    const void* wqkv;  const float* sqkv;    /* [q | k | v] rows */
+    const void* wo;    const float* so;
+    const void* wgu;   const float* sgu;     /* [gate | up] rows */
+    const void* wdown; const float* sdown;
+    const float* in_norm;
+    const float* post_norm;
+    const float* q_norm;
+    const float* k_norm;
+    uint16_t* kc;      /* [max_seq][nkv*hd] fp16 */
+    uint16_t* vc;
+} mdx_persist_layer;
+
+typedef struct {
+    int kind;              /* MDX_W_F16 / MDX_W_I8 / MDX_W_I4 for every projection */
+    int n_layers, vocab, max_seq, rope_style;
+    int head;              /* 1: final norm + INT8 lm_head + argmax; 0: layers only */
+    int advance;           /* state->pos += advance at the end of the step */
+    float eps;
+    mdx_state* state;
+    mdx_persist_layer l0;              /* layer 0; layer l's pointers are l0's plus
+                                          l * layer_stride bytes, its KV caches
+                                          l0.kc/vc plus l * kv_stride elements */
+    long long layer_stride;
+    long long kv_stride;
+    const float* emb_table;            /* [vocab][d] fp32 */
+    const float* emb_in;               /* [d], used when state->mode == 1 */
+    const float* cos_t;
+    const float* sin_t;
+    const float* final_norm;
+    const int8_t* lm_w;                /* [vocab][d] int8 */
+    const float* lm_scale;             /* [vocab] */
+    float* logits;                     /* [vocab] */
+    float* hidden_out;                 /* [d] final hidden (before the final norm) */
+    void* xbuf;                        /* mdx_persist_xbuf_bytes(), zeroed once at creation */
+    int* out_tokens;                   /* optional greedy output list (state->n_out) */
+} mdx_persist_args;
+
+/* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */
+int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F);
+/* 1 when the current device can hold the whole grid co-resident. */
+int mdx_persist_usable(int kind);
+size_t mdx_persist_xbuf_bytes(void);
+/* One decode step (all layers, and the lm_head when head != 0).  A wait that
+ * times out sets state->pad[1] = 1; the caller treats that as a failure. */
+int mdx_launch_persist_step(const mdx_persist_args* a, void* stream);
+
 /* ---- batch prefill (M <= 64) kernels ---- */
 
 /* x16[m][d] = fp16((x[m]*rms)*w) for m < M. */

@@ -1,0 +1,955 @@
+// mdx_persist.hip — one decode step of the 0.6B-class decoder (hidden 1024,
+// 16 query / 8 KV heads of 128, SwiGLU FFN 3072, INT8 lm_head) as a single
+// cooperative launch of 256 workgroups, one per CU.
+//
+// Reference path replaced: matmul_decoder_step (src/matmul_decoder.c:1430-1634):
+// embedding, per layer RMSNorm -> q/k/v -> QK-norm -> RoPE -> KV append ->
+// GQA attention -> o -> residual -> RMSNorm -> gate/up -> SwiGLU -> down ->
+// residual, then final norm, the INT8 lm_head and argmax_f32.
+//
+// A step of this model is a chain of six dependent exchanges per layer; each
+// one needs every workgroup's output before anyone can go on.  With one
+// kernel per stage every exchange costs a kernel boundary and every kernel
+// starts with an idle HBM pipe.  Here the workgroups stay resident and
+// exchange through "LL" words: 32-bit words holding 16 payload bits and a
+// 16-bit epoch, written with agent-coherent stores and polled with
+// L2-bypassing (sc1) 16-byte loads.  A reader knows a word is current when
+// its epoch matches, so there is no flag, fence or barrier round trip.  The
+// weights of the next stage are requested before each wait, so the HBM
+// stream runs while workgroups wait for each other.
+//
+// Work split (b = workgroup, t = thread):
+//   qkv    group j = b % 8 (one KV head), split s = b / 8: the 16 rows
+//          s*16.. of [q(2j) | q(2j+1) | k(j) | v(j)];
+//   attn   (j, s): positions [s*c, (s+1)*c) of KV head j, c = ceil(L/32),
+//          online softmax over the chunk -> partial (m, l, o);
+//   merge  (j, s): 8 of the 256 outputs of KV head j from the 32 partials;
+//   o      rows 4b..4b+3 (+ residual), gate/up: features 12b..12b+11,
+//   down   rows 4b..4b+3 (+ residual), lm_head: rows [bV/256, (b+1)V/256).
+// Every wait is bounded: a workgroup that times out records an error in
+// state->pad[1] and stops waiting, so the grid always drains.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "mdx_common.h"
+#include "mdx_device.h"
+
+using namespace mdx;
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int NB = 256;                 // workgroups
+constexpr int NT = 256;                 // threads per workgroup
+constexpr int D = 1024, NQ = 16, NKV = 8, HD = 128, FF = 3072;
+constexpr int QD = NQ * HD, KVD = NKV * HD;
+constexpr int GRP = NB / NKV;           // workgroups per KV head
+constexpr int PP = 4;                   // 16-position K/V passes requested ahead
+constexpr unsigned kSpinLimit = 1u << 18;
+
+// exchange buffer layout, in 32-bit words
+constexpr int W_CTRL = 0;                          // [0] step counter
+constexpr int W_QKV = 16;                          // [NKV][512 values][2]
+constexpr int PART_WORDS = 520;                    // m0 l0 m1 l1 (x2) | o0[128] x2 | o1[128] x2
+constexpr int W_PART = W_QKV + NKV * 1024;         // [NKV][GRP][PART_WORDS]
+constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [QD] fp16
+constexpr int W_HO = W_ATT + QD;                   // [D][2] hidden after o
+constexpr int W_ACT = W_HO + 2 * D;                // [FF] fp16
+constexpr int W_HD = W_ACT + FF;                   // [D][2] hidden after down
+constexpr int W_AMAX = W_HD + 2 * D;               // [NB][4] argmax keys
+constexpr int W_TOTAL = W_AMAX + NB * 4;
+static_assert(W_PART % 4 == 0 && W_ATT % 4 == 0 && W_HO % 4 == 0 && W_ACT % 4 == 0 &&
+              W_HD % 4 == 0 && W_AMAX % 4 == 0, "16-byte aligned regions");
+
+struct PArgs {
+    int n_layers, vocab, max_seq, rope_style, head, advance;
+    float eps;
+    mdx_state* st;
+    mdx_persist_layer l0;       // layer 0; layer l is l0 advanced by l * lstride bytes
+    long long lstride;          // (KV caches: by l * kvstride elements)
+    long long kvstride;
+    const float* emb_table;
+    const float* emb_in;
+    const float* cos_t;
+    const float* sin_t;
+    const float* final_norm;
+    const int8_t* lm_w;
+    const float* lm_scale;
+    float* logits;
+    float* hidden_out;
+    unsigned* xbuf;
+    int* out_tokens;
+};
+
+// ---- LL words ---------------------------------------------------------------
+
+// Cache policy sc1: bypass the non-coherent caches.  The buffer-load builtin
+// is a plain read to the optimiser, so the polling loop below carries a
+// compiler memory barrier to keep the reload inside the loop.
+__device__ __forceinline__ u32x4 ll_load(__amdgpu_buffer_rsrc_t rs, int word) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, 16);
+}
+__device__ __forceinline__ bool ll_ok(u32x4 v, unsigned ep) {
+    return ((v.x >> 16) == ep) & ((v.y >> 16) == ep) & ((v.z >> 16) == ep) & ((v.w >> 16) == ep);
+}
+__device__ __forceinline__ float ll_f32(unsigned lo, unsigned hi) {
+    return __uint_as_float((lo & 0xffffu) | (hi << 16));
+}
+__device__ __forceinline__ void ll_put(unsigned* xb, int word, unsigned payload, unsigned ep) {
+    __hip_atomic_store(xb + word, (payload & 0xffffu) | (ep << 16), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_put_f32(unsigned* xb, int word, float v, unsigned ep) {
+    const unsigned u = __float_as_uint(v);
+    ll_put(xb, word, u & 0xffffu, ep);
+    ll_put(xb, word + 1, u >> 16, ep);
+}
+
+// Polls N 16-byte groups until every word carries epoch ep.  Returns false
+// after kSpinLimit rounds (the data is then stale; the caller stops waiting).
+template <int N>
+__device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&word)[N],
+                                        u32x4 (&v)[N], unsigned ep, bool dead) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = ll_load(rs, word[i]);
+    if (dead) return true;
+    for (unsigned spin = 0;; spin++) {
+        asm volatile("" ::: "memory");
+        bool all = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            if (!ll_ok(v[i], ep)) {
+                all = false;
+                v[i] = ll_load(rs, word[i]);
+            }
+        }
+        if (all) return true;
+        if (spin > kSpinLimit) return false;
+    }
+}
+
+// Layer pointers are computed, not loaded: a load of them would be a vector
+// memory load (the kernel writes global memory, so the compiler cannot use
+// scalar loads) and would queue behind the weight stream.
+__device__ __forceinline__ mdx_persist_layer layer_at(const PArgs& a, int l) {
+    const size_t off = (size_t)l * (size_t)a.lstride;
+    auto adv = [off](const void* p) -> const void* {
+        return p ? reinterpret_cast<const char*>(p) + off : nullptr;
+    };
+    mdx_persist_layer r;
+    r.wqkv = adv(a.l0.wqkv);
+    r.sqkv = reinterpret_cast<const float*>(adv(a.l0.sqkv));
+    r.wo = adv(a.l0.wo);
+    r.so = reinterpret_cast<const float*>(adv(a.l0.so));
+    r.wgu = adv(a.l0.wgu);
+    r.sgu = reinterpret_cast<const float*>(adv(a.l0.sgu));
+    r.wdown = adv(a.l0.wdown);
+    r.sdown = reinterpret_cast<const float*>(adv(a.l0.sdown));
+    r.in_norm = reinterpret_cast<const float*>(adv(a.l0.in_norm));
+    r.post_norm = reinterpret_cast<const float*>(adv(a.l0.post_norm));
+    r.q_norm = reinterpret_cast<const float*>(adv(a.l0.q_norm));
+    r.k_norm = reinterpret_cast<const float*>(adv(a.l0.k_norm));
+    r.kc = a.l0.kc + (size_t)l * (size_t)a.kvstride;
+    r.vc = a.l0.vc + (size_t)l * (size_t)a.kvstride;
+    return r;
+}
+
+__device__ __forceinline__ unsigned step_epoch(unsigned E, int L, int l) {
+    return (unsigned)(((unsigned long long)E * (unsigned)(L + 2) + (unsigned)l) % 65535ull) + 1u;
+}
+
+// ---- weights ----------------------------------------------------------------
+
+template <int KIND> struct KT;
+template <> struct KT<MDX_W_F16> { static constexpr int E = 8; };
+template <> struct KT<MDX_W_I8> { static constexpr int E = 16; };
+template <> struct KT<MDX_W_I4> { static constexpr int E = 32; };
+
+// 16-byte weight chunk . activation chunk (E fp16 values = E/8 uint4).
+template <int KIND>
+__device__ __forceinline__ float wdot(uint4 w, const uint4* x, float acc) {
+    if constexpr (KIND == MDX_W_F16) {
+        return dot8_f16(w, x[0], acc);
+    } else if constexpr (KIND == MDX_W_I8) {
+        return dot16_i8(w, x[0], x[1], acc);
+    } else {
+        acc = dot8_i4(w.x, x[0], acc);
+        acc = dot8_i4(w.y, x[1], acc);
+        acc = dot8_i4(w.z, x[2], acc);
+        return dot8_i4(w.w, x[3], acc);
+    }
+}
+
+// Row-major slice: R rows of K; thread t owns chunk kc = t % CPR of rows
+// RPT*i + t / CPR, i < NW.  One wave load instruction reads 1 KiB of a row
+// (CPR >= 64) or two 512-byte halves (CPR == 32).
+template <int KIND, int R, int K>
+struct RowMajor {
+    static constexpr int E = KT<KIND>::E;
+    static constexpr int CPR = K / E;
+    static constexpr int RPT = NT / CPR;
+    static constexpr int NW = R / RPT;
+    static constexpr int G = CPR < 64 ? CPR : 64;          // lanes sharing a row set
+    static constexpr int NSPLIT = CPR > 64 ? CPR / 64 : 1; // waves sharing a row
+    static constexpr int NV = NW <= 1 ? 1 : (NW <= 2 ? 2 : (NW <= 4 ? 4 : (NW <= 8 ? 8 : 16)));
+    static_assert(NT % CPR == 0 && R % RPT == 0 && NW <= 16, "row-major slice shape");
+};
+
+// Chunk-major slice: R rows (R divides 64); thread t owns row t % R and
+// chunks t / R + (NT / R) * i, i < NW (the last ones may fall past the row).
+template <int KIND, int R, int K>
+struct ChunkMajor {
+    static constexpr int E = KT<KIND>::E;
+    static constexpr int CPR = K / E;
+    static constexpr int STEP = NT / R;
+    static constexpr int NW = (CPR + STEP - 1) / STEP;
+    static constexpr bool RAGGED = CPR % STEP != 0;
+};
+
+// Reduce-scatter of NV per-lane values over aligned groups of G lanes: on
+// return lane l holds the group total of value (l % G) / (G / NV).
+constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
+
+template <int NV, int G>
+__device__ __forceinline__ float reduce_scatter(float (&v)[NV], int lane) {
+    constexpr int STEPS = ilog2(G);
+#pragma unroll
+    for (int st = 0; st < STEPS; st++) {
+        const int o = G >> (st + 1);
+        const int nv = NV >> st;
+        if (nv > 1) {
+            const int half = nv / 2;
+            // bitwise select: keeps both reads static (a select of two array
+            // elements would otherwise become a dynamically indexed read)
+            const unsigned up = (lane & o) ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int k = 0; k < NV / 2; k++) {
+                if (k < half) {
+                    const unsigned lo = __float_as_uint(v[k]), hi = __float_as_uint(v[k + half]);
+                    const float send = __uint_as_float((lo & up) | (hi & ~up));
+                    const float keep = __uint_as_float((hi & up) | (lo & ~up));
+                    v[k] = keep + __shfl_xor(send, o, 64);
+                }
+            }
+        } else {
+            v[0] += __shfl_xor(v[0], o, 64);
+        }
+    }
+    return v[0];
+}
+
+// Row-major dot + reduction; red[r * NSPLIT + part] receives the row sums.
+template <int KIND, int R, int K, int NWT>
+__device__ __forceinline__ void rm_dot(const uint4 (&w)[NWT], const uint4* xs4, float* red, int t) {
+    using S = RowMajor<KIND, R, K>;
+    static_assert(NWT == S::NW, "weight register count");
+    constexpr int XC = S::E / 8;
+    const int kc = t % S::CPR, rsub = t / S::CPR, lane = t & 63;
+    uint4 xr[XC];
+#pragma unroll
+    for (int e = 0; e < XC; e++) xr[e] = xs4[kc * XC + e];
+    float v[S::NV];
+#pragma unroll
+    for (int i = 0; i < S::NV; i++) v[i] = i < S::NW ? wdot<KIND>(w[i < S::NW ? i : 0], xr, 0.0f) : 0.0f;
+    const float tot = reduce_scatter<S::NV, S::G>(v, lane);
+    constexpr int PER = S::G / S::NV;
+    const int idx = (lane % S::G) / PER;
+    if ((lane % PER) == 0 && idx < S::NW)
+        red[(S::RPT * idx + rsub) * S::NSPLIT + (kc / 64)] = tot;
+}
+
+template <int KIND, int R, int K, int NWT, typename RowFn>
+__device__ __forceinline__ void rm_load(uint4 (&w)[NWT], const void* W, RowFn row_of, int t,
+                                        int i0, int i1) {
+    using S = RowMajor<KIND, R, K>;
+    static_assert(NWT == S::NW, "weight register count");
+    const int kc = t % S::CPR, rsub = t / S::CPR;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(W) + kc * 16;
+#pragma unroll
+    for (int i = 0; i < S::NW; i++) {
+        if (i >= i0 && i < i1)
+            w[i] = *reinterpret_cast<const uint4*>(base + (size_t)row_of(S::RPT * i + rsub) * (S::CPR * 16));
+    }
+}
+
+template <int KIND, int R, int K, int NWT>
+__device__ __forceinline__ void cm_load(uint4 (&w)[NWT], const void* W, int row0, int t) {
+    using S = ChunkMajor<KIND, R, K>;
+    static_assert(NWT == S::NW, "weight register count");
+    const int r = t % R;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(W) + (size_t)(row0 + r) * (S::CPR * 16);
+#pragma unroll
+    for (int i = 0; i < S::NW; i++) {
+        // chunks past the row load chunk 0 instead; cm_dot skips them
+        int kc = t / R + S::STEP * i;
+        if (S::RAGGED && kc >= S::CPR) kc = 0;
+        w[i] = *reinterpret_cast<const uint4*>(base + kc * 16);
+    }
+}
+
+// Chunk-major dot + reduction over lanes with equal t % R; red[wave * R + r].
+template <int KIND, int R, int K, int NWT>
+__device__ __forceinline__ void cm_dot(const uint4 (&w)[NWT], const uint4* xs4, float* red, int t) {
+    using S = ChunkMajor<KIND, R, K>;
+    static_assert(NWT == S::NW, "weight register count");
+    constexpr int XC = S::E / 8;
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S::NW; i++) {
+        const int kc = t / R + S::STEP * i;
+        if (!S::RAGGED || kc < S::CPR) acc = wdot<KIND>(w[i], xs4 + kc * XC, acc);
+    }
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    const int lane = t & 63;
+    if (lane < R) red[(t >> 6) * R + lane] = acc;
+}
+
+// ---- small helpers ----------------------------------------------------------
+
+__device__ __forceinline__ float block_sum4(float v, float* ws, int t) {
+    v = wave_sum(v);
+    if ((t & 63) == 0) ws[t >> 6] = v;
+    __syncthreads();
+    return (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+// fp16 x[4t..4t+4) = fp16((h * rms) * w) into the LDS activation vector.
+__device__ __forceinline__ void norm_to_x(const float (&h)[4], float4 w, float rms, uint4* xs4,
+                                          int t) {
+    uint2 p;
+    p.x = (uint32_t)f32_to_f16_bits((h[0] * rms) * w.x) | ((uint32_t)f32_to_f16_bits((h[1] * rms) * w.y) << 16);
+    p.y = (uint32_t)f32_to_f16_bits((h[2] * rms) * w.z) | ((uint32_t)f32_to_f16_bits((h[3] * rms) * w.w) << 16);
+    reinterpret_cast<uint2*>(xs4)[t] = p;
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
+}
+
+// QK-norm (optional) + RoPE of one 128-wide head held in LDS, one wave.
+// With cache != NULL the results are rounded to fp16, stored there, and the
+// rounded values kept (the fp16 KV-cache semantic).
+__device__ __forceinline__ void rope_head(const float* src, const float* nw, float eps,
+                                          const float* cr, const float* sr, int style, float* dst,
+                                          uint16_t* cache, int lane) {
+    constexpr int half = HD / 2;
+    float rms = 1.0f;
+    if (nw) {
+        float ss = src[lane] * src[lane] + src[lane + 64] * src[lane + 64];
+        ss = wave_sum(ss);
+        rms = 1.0f / sqrtf(ss / (float)HD + eps);
+    }
+    const int i = lane;
+    const int i0 = style == 0 ? 2 * i : i;
+    const int i1 = style == 0 ? 2 * i + 1 : i + half;
+    float x0 = src[i0], x1 = src[i1];
+    if (nw) {
+        x0 = (x0 * rms) * nw[i0];
+        x1 = (x1 * rms) * nw[i1];
+    }
+    const float c = cr[i], s = sr[i];
+    float o0 = x0 * c - x1 * s;
+    float o1 = x1 * c + x0 * s;
+    if (cache) {
+        const uint16_t h0 = f32_to_f16_bits(o0), h1 = f32_to_f16_bits(o1);
+        cache[i0] = h0;
+        cache[i1] = h1;
+        o0 = f16_bits_to_f32(h0);
+        o1 = f16_bits_to_f32(h1);
+    }
+    dst[i0] = o0;
+    dst[i1] = o1;
+}
+
+__device__ __forceinline__ void h8_to_f32(uint4 u, float (&f)[8]) {
+    const half2_t a = as_h2(u.x), b = as_h2(u.y), c = as_h2(u.z), d = as_h2(u.w);
+    f[0] = (float)a.x; f[1] = (float)a.y; f[2] = (float)b.x; f[3] = (float)b.y;
+    f[4] = (float)c.x; f[5] = (float)c.y; f[6] = (float)d.x; f[7] = (float)d.y;
+}
+
+// Online-softmax update of one position for the two query heads of a thread.
+__device__ __forceinline__ void attn_update(const float (&q)[2][8], const float (&kf)[8],
+                                            const float (&vf)[8], bool valid, float (&m)[2],
+                                            float (&l)[2], float (&o)[2][8]) {
+    const float scale = 0.08838834764831845f;   // 1/sqrt(128)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float s = q[h][0] * kf[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) s = s + q[h][e] * kf[e];
+        s = group_sum(s, 16) * scale;
+        if (valid) {
+            const float mn = fmaxf(m[h], s);
+            const float a = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn);
+            const float p = expf(s - mn);
+            l[h] = l[h] * a + p;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[h][e] = o[h][e] * a + p * vf[e];
+            m[h] = mn;
+        }
+    }
+}
+
+__device__ __forceinline__ void ml_merge(float& m, float& l, float* o, int n, float m2, float l2,
+                                         const float* o2) {
+    const float M = fmaxf(m, m2);
+    if (M == -INFINITY) return;
+    const float a = m == -INFINITY ? 0.0f : expf(m - M);
+    const float b = m2 == -INFINITY ? 0.0f : expf(m2 - M);
+    l = l * a + l2 * b;
+    for (int e = 0; e < n; e++) o[e] = o[e] * a + o2[e] * b;
+    m = M;
+}
+
+// ---- the step kernel --------------------------------------------------------
+
+template <int KIND>
+__global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
+    using SA = RowMajor<KIND, 16, D>;       // qkv
+    using SE = RowMajor<KIND, 24, D>;       // gate/up
+    using SD = ChunkMajor<KIND, 4, QD>;     // o
+    using SF = ChunkMajor<KIND, 4, FF>;     // down
+
+    __shared__ uint4 xs4[FF / 8];
+    __shared__ float red[64];
+    __shared__ float ws[8];
+    __shared__ float hres[4];
+    __shared__ float gu_s[24];
+    __shared__ float qkv_s[512];
+    __shared__ float q_s[2 * HD];
+    __shared__ float kn_s[HD];
+    __shared__ float vn_s[HD];
+    __shared__ float wpart[4][2][HD + 2];
+    __shared__ unsigned long long bkey[4];
+
+    const int t = threadIdx.x, b = blockIdx.x, lane = t & 63, wave = t >> 6;
+    const int L = a.n_layers;
+    unsigned* xb = a.xbuf;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(xb, (short)0, W_TOTAL * 4, 0x00020000);
+
+    const unsigned E = __hip_atomic_load(xb + W_CTRL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int pos = a.st->pos;
+    const int mode = a.st->mode;
+    int tok = a.st->token;
+    bool dead = false;
+
+    // attention work split of this workgroup
+    const int j = b % NKV, s = b / NKV;
+    const int Lk = pos + 1;
+    const int cks = (Lk + GRP - 1) / GRP;
+    const int p0 = s * cks;
+    const int p1 = min(Lk, p0 + cks);
+    const int n = p1 > p0 ? p1 - p0 : 0;
+    const bool has_new = pos >= p0 && pos < p1;
+    const int pl = t >> 4, dl = t & 15;
+
+    // qkv row map: 16 consecutive rows of one head
+    const int seg = s >> 3, r0 = (s & 7) * 16;
+    const int qkv_row0 = seg == 0 ? (2 * j) * HD + r0
+                       : seg == 1 ? (2 * j + 1) * HD + r0
+                       : seg == 2 ? QD + j * HD + r0
+                                  : QD + KVD + j * HD + r0;
+    auto rowA = [&](int r) { return qkv_row0 + r; };
+    auto rowE = [&](int r) { return r < 12 ? 12 * b + r : FF + 12 * b + (r - 12); };
+
+    uint4 wA[SA::NW];
+    rm_load<KIND, 16, D>(wA, a.l0.wqkv, rowA, t, 0, SA::NW);
+
+    // layer-0 input: the token's embedding row (or the uploaded embedding)
+    float h[4];
+    {
+        tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
+        const float* src = mode == 1 ? a.emb_in : a.emb_table + (size_t)tok * D;
+        const float4 v = reinterpret_cast<const float4*>(src)[t];
+        h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+    }
+
+    for (int l = 0; l < L; l++) {
+        const mdx_persist_layer Ly = layer_at(a, l);
+        const unsigned ep = step_epoch(E, L, l);
+        const unsigned ep_prev = step_epoch(E, L, l - 1 < 0 ? 0 : l - 1);
+
+        // ================= A: RMSNorm + qkv =================
+        uint4 kr[PP], vr[PP];
+#pragma unroll
+        for (int q = 0; q < PP; q++) {
+            // unconditional loads (row 0 stands in for unused slots), so the
+            // requests are not tied to a branch that waits for them
+            const int pi = 16 * q + pl;
+            const int p = p0 + pi;
+            const int pc = (pi < n && p != pos) ? p : 0;
+            kr[q] = *reinterpret_cast<const uint4*>(Ly.kc + (size_t)pc * KVD + j * HD + dl * 8);
+            vr[q] = *reinterpret_cast<const uint4*>(Ly.vc + (size_t)pc * KVD + j * HD + dl * 8);
+        }
+        uint4 wD[SD::NW];
+        cm_load<KIND, 4, QD>(wD, Ly.wo, 4 * b, t);
+        const float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
+        const float sclA = Ly.sqkv ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
+        if (l > 0) {
+            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
+            u32x4 v[2];
+            const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead);
+            h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
+            h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
+        {
+            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+            const float tot = block_sum4(ss, ws, t);
+            const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
+            norm_to_x(h, nwA, rms, xs4, t);
+        }
+        __syncthreads();
+        rm_dot<KIND, 16, D>(wA, xs4, red, t);
+        __syncthreads();
+        if (t < 16) {
+            float y = red[t * SA::NSPLIT];
+            if (SA::NSPLIT == 2) y = y + red[t * SA::NSPLIT + 1];
+            y = y * sclA;
+            ll_put_f32(xb, W_QKV + j * 1024 + 2 * (s * 16 + t), y, ep);
+        }
+
+        // ================= B: QK-norm, RoPE, KV append, partial attention ==========
+        uint4 wE[SE::NW];
+        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, 0, SE::NW / 2);
+        const float* cr = a.cos_t + (size_t)pos * (HD / 2);
+        const float* sr = a.sin_t + (size_t)pos * (HD / 2);
+        {
+            int wd[1] = {W_QKV + j * 1024 + 4 * t};
+            u32x4 v[1];
+            const bool ok = ll_wait<1>(rs, wd, v, ep, dead);
+            qkv_s[2 * t] = ll_f32(v[0].x, v[0].y);
+            qkv_s[2 * t + 1] = ll_f32(v[0].z, v[0].w);
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        if (wave < 2) {
+            rope_head(qkv_s + wave * HD, Ly.q_norm, a.eps, cr, sr, a.rope_style, q_s + wave * HD,
+                      nullptr, lane);
+        } else if (has_new && wave == 2) {
+            rope_head(qkv_s + 2 * HD, Ly.k_norm, a.eps, cr, sr, a.rope_style, kn_s,
+                      Ly.kc + (size_t)pos * KVD + j * HD, lane);
+        } else if (has_new) {
+            for (int e = lane; e < HD; e += 64) {
+                const uint16_t hv = f32_to_f16_bits(qkv_s[3 * HD + e]);
+                Ly.vc[(size_t)pos * KVD + j * HD + e] = hv;
+                vn_s[e] = f16_bits_to_f32(hv);
+            }
+        }
+        __syncthreads();
+        {
+            float q[2][8];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) q[hh][e] = q_s[hh * HD + dl * 8 + e];
+            float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.0f, 0.0f};
+            float o[2][8];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
+            auto pass = [&](uint4 kk, uint4 vv, int pi) {
+                const int p = p0 + pi;
+                const bool valid = pi < n;
+                float kf[8], vf[8];
+                if (valid && p == pos) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) { kf[e] = kn_s[dl * 8 + e]; vf[e] = vn_s[dl * 8 + e]; }
+                } else {
+                    h8_to_f32(kk, kf);
+                    h8_to_f32(vv, vf);
+                }
+                attn_update(q, kf, vf, valid, m, lsum, o);
+            };
+#pragma unroll
+            for (int qq = 0; qq < PP; qq++) pass(kr[qq], vr[qq], 16 * qq + pl);
+            for (int q0 = PP; 16 * q0 < n; q0 += PP) {      // chunks longer than 16*PP
+                uint4 kx[PP], vx[PP];
+#pragma unroll
+                for (int qq = 0; qq < PP; qq++) {
+                    const int pi = 16 * (q0 + qq) + pl;
+                    const int p = p0 + pi;
+                    const int pc = (pi < n && p != pos) ? p : 0;
+                    kx[qq] = *reinterpret_cast<const uint4*>(Ly.kc + (size_t)pc * KVD + j * HD + dl * 8);
+                    vx[qq] = *reinterpret_cast<const uint4*>(Ly.vc + (size_t)pc * KVD + j * HD + dl * 8);
+                }
+#pragma unroll
+                for (int qq = 0; qq < PP; qq++) pass(kx[qq], vx[qq], 16 * (q0 + qq) + pl);
+            }
+            // merge the 4 position groups of each wave (lane bits 4 and 5)
+#pragma unroll
+            for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    const float m2 = __shfl_xor(m[hh], off, 64);
+                    const float l2 = __shfl_xor(lsum[hh], off, 64);
+                    float o2[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o2[e] = __shfl_xor(o[hh][e], off, 64);
+                    ml_merge(m[hh], lsum[hh], o[hh], 8, m2, l2, o2);
+                }
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) wpart[wave][hh][dl * 8 + e] = o[hh][e];
+                    if (lane == 0) {
+                        wpart[wave][hh][HD] = m[hh];
+                        wpart[wave][hh][HD + 1] = lsum[hh];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        {
+            const int hh = t >> 7, d = t & 127;
+            float M = wpart[0][hh][HD], Ls = wpart[0][hh][HD + 1], O = wpart[0][hh][d];
+#pragma unroll
+            for (int w = 1; w < 4; w++)
+                ml_merge(M, Ls, &O, 1, wpart[w][hh][HD], wpart[w][hh][HD + 1], &wpart[w][hh][d]);
+            const int base = W_PART + (j * GRP + s) * PART_WORDS;
+            ll_put_f32(xb, base + 8 + 256 * hh + 2 * d, O, ep);
+            if (d == 0) {
+                ll_put_f32(xb, base + 4 * hh, M, ep);
+                ll_put_f32(xb, base + 4 * hh + 2, Ls, ep);
+            }
+        }
+
+        // ================= C: merge the 32 partials of KV head j ==========
+        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+        {
+            const int hh = s >> 4, d0 = (s & 15) * 8;
+            bool ok = true;
+            float m = -INFINITY, lsum = 0.0f, o[8];
+            if (t < 32) {
+                const int base = W_PART + (j * GRP + t) * PART_WORDS;
+                int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0,
+                             base + 12 + 256 * hh + 2 * d0, base + 16 + 256 * hh + 2 * d0,
+                             base + 20 + 256 * hh + 2 * d0};
+                u32x4 v[5];
+                ok = ll_wait<5>(rs, wd, v, ep, dead);
+                m = ll_f32(v[0].x, v[0].y);
+                lsum = ll_f32(v[0].z, v[0].w);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    o[2 * k] = ll_f32(v[1 + k].x, v[1 + k].y);
+                    o[2 * k + 1] = ll_f32(v[1 + k].z, v[1 + k].w);
+                }
+            }
+            if (t < 64) {
+                // lanes 32..63 hold empty partials (m = -inf)
+                float M = m;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+                const float wgt = m == -INFINITY ? 0.0f : expf(m - M);
+                float acc[9];
+                acc[8] = t < 32 ? lsum * wgt : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] = t < 32 ? o[e] * wgt : 0.0f;
+#pragma unroll
+                for (int off = 1; off < 32; off <<= 1)
+#pragma unroll
+                    for (int e = 0; e < 9; e++) acc[e] += __shfl_xor(acc[e], off, 64);
+                if (t < 8) {
+                    float val = acc[0];
+#pragma unroll
+                    for (int e = 1; e < 8; e++) val = t == e ? acc[e] : val;
+                    ll_put(xb, W_ATT + (2 * j + hh) * HD + d0 + t, f32_to_f16_bits(val / acc[8]), ep);
+                }
+            }
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+
+        // ================= D: o projection + residual ==========
+        uint4 wF[SF::NW];
+        cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
+        const float sclD = Ly.so ? Ly.so[4 * b + (t & 3)] : 1.0f;
+        {
+            int wd[2] = {W_ATT + 8 * t, W_ATT + 8 * t + 4};
+            u32x4 v[2];
+            const bool ok = ll_wait<2>(rs, wd, v, ep, dead);
+            uint4 x;
+            x.x = (v[0].x & 0xffffu) | (v[0].y << 16);
+            x.y = (v[0].z & 0xffffu) | (v[0].w << 16);
+            x.z = (v[1].x & 0xffffu) | (v[1].y << 16);
+            x.w = (v[1].z & 0xffffu) | (v[1].w << 16);
+            xs4[t] = x;
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        cm_dot<KIND, 4, QD>(wD, xs4, red, t);
+        __syncthreads();
+        if (t < 4) {
+            const float y = ((red[t] + red[4 + t]) + (red[8 + t] + red[12 + t])) * sclD;
+            ll_put_f32(xb, W_HO + 2 * (4 * b + t), hres[t] + y, ep);
+        }
+
+        // ================= E: RMSNorm + gate/up + SwiGLU ==========
+        const bool last = l + 1 == L;
+        if (!last) rm_load<KIND, 16, D>(wA, layer_at(a, l + 1).wqkv, rowA, t, 0, SA::NW);
+        const float4 nwE = reinterpret_cast<const float4*>(Ly.post_norm)[t];
+        const float sclE = Ly.sgu ? Ly.sgu[rowE(t < 24 ? t : 0)] : 1.0f;
+        {
+            int wd[2] = {W_HO + 8 * t, W_HO + 8 * t + 4};
+            u32x4 v[2];
+            const bool ok = ll_wait<2>(rs, wd, v, ep, dead);
+            h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
+            h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
+        {
+            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+            const float tot = block_sum4(ss, ws + 4, t);
+            const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
+            norm_to_x(h, nwE, rms, xs4, t);
+        }
+        __syncthreads();
+        rm_dot<KIND, 24, D>(wE, xs4, red, t);
+        __syncthreads();
+        if (t < 24) {
+            float y = red[t * SE::NSPLIT];
+            if (SE::NSPLIT == 2) y = y + red[t * SE::NSPLIT + 1];
+            gu_s[t] = y * sclE;
+        }
+        __syncthreads();
+        if (t < 12) {
+            const float g = gu_s[t], u = gu_s[12 + t];
+            ll_put(xb, W_ACT + 12 * b + t, f32_to_f16_bits(silu_mul(g, u)), ep);
+        }
+
+        // ================= F: down projection + residual ==========
+        const float sclF = Ly.sdown ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
+        {
+            int wd[3] = {W_ACT + 12 * t, W_ACT + 12 * t + 4, W_ACT + 12 * t + 8};
+            u32x4 v[3];
+            const bool ok = ll_wait<3>(rs, wd, v, ep, dead);
+            uint2* x2 = reinterpret_cast<uint2*>(xs4);
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                uint2 p;
+                p.x = (v[k].x & 0xffffu) | (v[k].y << 16);
+                p.y = (v[k].z & 0xffffu) | (v[k].w << 16);
+                x2[3 * t + k] = p;
+            }
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        cm_dot<KIND, 4, FF>(wF, xs4, red, t);
+        __syncthreads();
+        if (t < 4) {
+            const float y = ((red[t] + red[4 + t]) + (red[8 + t] + red[12 + t])) * sclF;
+            const float hn = hres[t] + y;
+            ll_put_f32(xb, W_HD + 2 * (4 * b + t), hn, ep);
+            if (last) a.hidden_out[4 * b + t] = hn;
+        }
+        __syncthreads();   // hres / red reuse
+    }
+
+    const unsigned ep_last = step_epoch(E, L, L - 1);
+    const unsigned ep_head = step_epoch(E, L, L);
+    if (a.head) {
+        // ================= lm_head (INT8 rows, fp16 activations) + argmax ==========
+        constexpr int U = 16;
+        const int rb = (int)(((long long)b * a.vocab) / NB);
+        const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
+        const int8_t* W = a.lm_w;
+        auto load_rows = [&](uint4 (&w)[U], float& sc, int base) {
+            // rows past the block's range re-read row re-1; consume skips them
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int r = min(base + u, re - 1);
+                w[u] = *reinterpret_cast<const uint4*>(W + (size_t)r * D + lane * 16);
+            }
+            sc = a.lm_scale[min(base + (lane >> 2), re - 1)];
+        };
+        uint4 w0[U], w1[U];
+        float sc0 = 0.0f, sc1 = 0.0f;
+        load_rows(w0, sc0, rb + wave * U);
+        const float4 nw = reinterpret_cast<const float4*>(a.final_norm)[t];
+        {
+            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
+            u32x4 v[2];
+            const bool ok = ll_wait<2>(rs, wd, v, ep_last, dead);
+            h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
+            h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        {
+            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
+            const float tot = block_sum4(ss, ws, t);
+            const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
+            norm_to_x(h, nw, rms, xs4, t);
+        }
+        __syncthreads();
+        const uint4 x0 = xs4[2 * lane], x1 = xs4[2 * lane + 1];
+        unsigned long long best = 0ull;
+        auto consume = [&](const uint4 (&w)[U], float sc, int base) {
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) v[u] = dot16_i8(w[u], x0, x1, 0.0f);
+            const float tot = reduce_scatter<U, 64>(v, lane);
+            const int r = base + (lane >> 2);
+            if ((lane & 3) == 0 && r < re) {
+                const float y = tot * sc;
+                a.logits[r] = y;
+                if (y == y) {
+                    const unsigned long long k = argmax_key(y, r);
+                    best = k > best ? k : best;
+                }
+            }
+        };
+        for (int base = rb + wave * U; base < re; base += 8 * U) {
+            const int nb1 = base + 4 * U;
+            if (nb1 < re) load_rows(w1, sc1, nb1);
+            consume(w0, sc0, base);
+            if (nb1 >= re) break;
+            const int nb2 = nb1 + 4 * U;
+            if (nb2 < re) load_rows(w0, sc0, nb2);
+            consume(w1, sc1, nb1);
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const unsigned lo = __shfl_xor((unsigned)(best & 0xffffffffull), off, 64);
+            const unsigned hi = __shfl_xor((unsigned)(best >> 32), off, 64);
+            const unsigned long long k = ((unsigned long long)hi << 32) | lo;
+            best = k > best ? k : best;
+        }
+        if (lane == 0) bkey[wave] = best;
+        __syncthreads();
+        if (t == 0) {
+            unsigned long long k = bkey[0];
+            for (int w = 1; w < 4; w++) k = bkey[w] > k ? bkey[w] : k;
+            const unsigned hi = (unsigned)(k >> 32), lo = (unsigned)k;
+            const int base = W_AMAX + 4 * b;
+            ll_put(xb, base + 0, hi & 0xffffu, ep_head);
+            ll_put(xb, base + 1, hi >> 16, ep_head);
+            ll_put(xb, base + 2, lo & 0xffffu, ep_head);
+            ll_put(xb, base + 3, lo >> 16, ep_head);
+        }
+        if (b != 0) {
+            if (dead && t == 0)
+                __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        __syncthreads();   // bkey is reused below
+        unsigned long long k = 0ull;
+        {
+            int wd[1] = {W_AMAX + 4 * t};
+            u32x4 v[1];
+            const bool ok = ll_wait<1>(rs, wd, v, ep_head, dead);
+            const unsigned hi = (v[0].x & 0xffffu) | (v[0].y << 16);
+            const unsigned lo = (v[0].z & 0xffffu) | (v[0].w << 16);
+            k = ((unsigned long long)hi << 32) | lo;
+            if (!ok) dead = true;
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const unsigned lo = __shfl_xor((unsigned)(k & 0xffffffffull), off, 64);
+            const unsigned hi = __shfl_xor((unsigned)(k >> 32), off, 64);
+            const unsigned long long k2 = ((unsigned long long)hi << 32) | lo;
+            k = k2 > k ? k2 : k;
+        }
+        if (lane == 0) bkey[wave] = k;
+        if (__syncthreads_or(dead)) dead = true;
+        if (t == 0) {
+            unsigned long long kk = bkey[0];
+            for (int w = 1; w < 4; w++) kk = bkey[w] > kk ? bkey[w] : kk;
+            const int res = kk ? (int)(0xFFFFFFFFu - (unsigned)(kk & 0xFFFFFFFFull)) : 0;
+            mdx_state* st = a.st;
+            st->argmax = res;
+            st->token = res;
+            st->mode = 0;
+            if (a.out_tokens) {
+                a.out_tokens[st->n_out] = res;
+                st->n_out = st->n_out + 1;
+            }
+            st->pos = pos + a.advance;
+            if (dead) __hip_atomic_store(&st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(xb + W_CTRL, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+        if (dead && t == 0) __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (b == 0 && t == 0) {
+            a.st->pos = pos + a.advance;
+            __hip_atomic_store(xb + W_CTRL, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    (void)ep_last;
+}
+
+typedef void (*PersistKernel)(PArgs);
+
+PersistKernel pick(int kind) {
+    switch (kind) {
+        case MDX_W_F16: return k_persist_step<MDX_W_F16>;
+        case MDX_W_I8: return k_persist_step<MDX_W_I8>;
+        case MDX_W_I4: return k_persist_step<MDX_W_I4>;
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F) {
+    return d == D && nq == NQ && nkv == NKV && hd == HD && F == FF;
+}
+
+size_t mdx_persist_xbuf_bytes(void) { return (size_t)W_TOTAL * 4; }
+
+int mdx_persist_usable(int kind) {
+    PersistKernel k = pick(kind);
+    if (!k) return 0;
+    int dev = 0, coop = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop)
+        return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), NT, 0) !=
+        hipSuccess)
+        return 0;
+    return (long)per_cu * cus >= NB;
+}
+
+int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
+    PersistKernel k = pick(p->kind);
+    if (!k || p->n_layers <= 0 || !p->state || !p->xbuf || !p->l0.wqkv) return -1;
+    if (p->head && (!p->lm_w || !p->lm_scale || !p->logits || !p->final_norm)) return -1;
+    PArgs a;
+    a.n_layers = p->n_layers;
+    a.vocab = p->vocab;
+    a.max_seq = p->max_seq;
+    a.rope_style = p->rope_style;
+    a.head = p->head;
+    a.advance = p->advance;
+    a.eps = p->eps;
+    a.st = p->state;
+    a.l0 = p->l0;
+    a.lstride = p->layer_stride;
+    a.kvstride = p->kv_stride;
+    a.emb_table = p->emb_table;
+    a.emb_in = p->emb_in;
+    a.cos_t = p->cos_t;
+    a.sin_t = p->sin_t;
+    a.final_norm = p->final_norm;
+    a.lm_w = p->lm_w;
+    a.lm_scale = p->lm_scale;
+    a.logits = p->logits;
+    a.hidden_out = p->hidden_out;
+    a.xbuf = reinterpret_cast<unsigned*>(p->xbuf);
+    a.out_tokens = p->out_tokens;
+    void* args[] = {&a};
+    hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k), dim3(NB), dim3(NT),
+                                              args, 0, (hipStream_t)stream);
+    return e == hipSuccess ? 0 : -1;
+}
+
+}  // extern "C"

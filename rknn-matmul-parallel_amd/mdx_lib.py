@@ -107,6 +107,7 @@ def lib() -> C.CDLL:
             "mdx_device_count": (C.c_int, []),
             "mdx_last_error": (C.c_char_p, []),
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
+            "mdx_decode_path": (C.c_int, [P]),
             "mdx_kv_fill_normal": (C.c_int, [P, C.c_int, C.c_uint64]),
             "mdx_kv_read": (C.c_int, [P, C.c_int, C.c_int, C.c_int, _F, _F]),
             "mdx_prefill_logits": (C.c_int, [P, _F, C.c_int, _F]),
@@ -282,6 +283,11 @@ class Decoder:
         self.kvd = c.num_kv_heads * c.head_dim
         self.n_lm = c.num_lm_heads
         self.lm_vocab = c.lm_head_vocab_size if c.num_lm_heads > 1 else c.vocab_size
+
+    @property
+    def path(self) -> int:
+        """1: one cooperative launch per step; 0: per-stage kernels."""
+        return lib().mdx_decode_path(self.h)
 
     def close(self):
         if self.h:

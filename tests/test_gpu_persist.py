@@ -1,0 +1,133 @@
+"""The one-launch decode step (all layers, the lm_head and the argmax in one
+cooperative launch) on the 0.6B layer shape: d=1024, 16Q/8KV heads of 128,
+FFN 3072, with 2 layers and a 5000-row INT8 lm_head (not a multiple of the
+256 workgroups, so the row ranges are ragged).
+
+Checked against the oracle on the same seeded model files and KV contents,
+and against the per-stage kernel path of the same library (MDX_PERSIST=0 at
+context creation):
+- logits cosine >= 0.9999 and max relative error <= 2e-3, same argmax;
+- the K/V row appended at the step's position;
+- cache lengths that exercise every attention chunking case: 0 (only the new
+  position), 1, 33, 511, 600, 2100 (chunks longer than the 64 prefetched
+  positions) and 4100;
+- an uploaded embedding instead of a token, a step without the lm_head, and
+  16 greedy steps fed back on the device.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import cosine, rel_err
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = dict(hidden_dim=1024, num_q_heads=16, num_kv_heads=8, head_dim=128, ffn_dim=3072,
+             num_layers=2, vocab_size=5000, max_seq_len=4224, rms_eps=1e-6, rope_theta=1e6,
+             tie_word_embeddings=1, has_qk_norm=1, rope_style=1, max_batch_prefill=64)
+QUANTS = {0: "fp16", 1: "int8", 2: "int4"}
+MAX_SEQ = 4224
+
+
+@pytest.fixture(scope="module")
+def models(mdx, workdir):
+    cfg = mdx.qwen3_0_6b_config(name="persist-2l", **SHAPE)
+    made = {}
+
+    def get(quant):
+        if quant not in made:
+            path = os.path.join(workdir, f"persist_q{quant}")
+            mdx.write_model(path, cfg, quant, 2000 + quant)
+            made[quant] = path
+        return made[quant]
+    return cfg, get
+
+
+def _pair(mdx, oracle_lib, cfg, path, quant, persist=True):
+    old = os.environ.get("MDX_PERSIST")
+    os.environ["MDX_PERSIST"] = "1" if persist else "0"
+    try:
+        g = mdx.Decoder(path, cfg, QUANTS[quant], MAX_SEQ)
+    finally:
+        if old is None:
+            del os.environ["MDX_PERSIST"]
+        else:
+            os.environ["MDX_PERSIST"] = old
+    assert g.path == (1 if persist else 0)
+    o = oracle_lib.Model(path, SHAPE, quant, MAX_SEQ, kv_fp16=True)
+    return g, o
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
+@pytest.mark.parametrize("n_pos", [0, 1, 33, 511, 600, 2100, 4100])
+def test_step_matches_oracle(mdx, gpu, oracle_lib, models, quant, n_pos):
+    cfg, get = models
+    path = get(quant)
+    g, o = _pair(mdx, oracle_lib, cfg, path, quant)
+    seed = 77 + n_pos
+    if n_pos:
+        g.kv_fill_normal(n_pos, seed)
+        assert o.kv_fill_normal(n_pos, seed) == 0
+    tok = 4321
+    tg, lg = g.step(tok)
+    to, lo = o.step(tok)
+    c, r = cosine(lg, lo), rel_err(lg, lo)
+    print(f"q{quant} pos {n_pos}: gpu {tg} oracle {to} cos {c:.7f} rel {r:.2e}")
+    assert c >= 0.9999 and r <= 2e-3
+    assert tg == to == int(np.argmax(lo))
+    for layer in range(2):
+        kg, vg = g.kv_read(layer, n_pos, 1)
+        ko, vo = o.kv_read(layer, n_pos, 1)
+        assert np.allclose(kg, ko, rtol=4e-3, atol=4e-3), f"layer {layer} K row {n_pos}"
+        assert np.allclose(vg, vo, rtol=4e-3, atol=4e-3), f"layer {layer} V row {n_pos}"
+    assert g.seq_len == n_pos + 1
+
+
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_one_launch_matches_per_stage_path(mdx, gpu, oracle_lib, models, quant):
+    cfg, get = models
+    path = get(quant)
+    g1, _ = _pair(mdx, oracle_lib, cfg, path, quant, persist=True)
+    g0, _ = _pair(mdx, oracle_lib, cfg, path, quant, persist=False)
+    for g in (g0, g1):
+        g.kv_fill_normal(700, 5)
+    for tok in (17, 4999, 0):
+        t1, l1 = g1.step(tok)
+        t0, l0 = g0.step(tok)
+        print(f"q{quant} tok {tok}: cos {cosine(l1, l0):.8f} rel {rel_err(l1, l0):.2e}")
+        assert t1 == t0 and cosine(l1, l0) >= 0.99999 and rel_err(l1, l0) <= 1e-3
+
+
+def test_uploaded_embedding_and_headless_step(mdx, gpu, oracle_lib, models):
+    cfg, get = models
+    path = get(1)
+    g, o = _pair(mdx, oracle_lib, cfg, path, 1)
+    g.kv_fill_normal(64, 9)
+    assert o.kv_fill_normal(64, 9) == 0
+    emb = mdx.synth_fill_normal(1024, mdx.synth_seed(9, "persist/emb")) * 0.05
+    # a step without the lm_head only appends K/V and advances the position
+    tg, lg = g.step(12, logits=False)
+    to, _ = o.step(12, logits=False)
+    assert lg is None and g.seq_len == 65
+    tg, lg = g.step(0, embedding=emb)
+    to, lo = o.step(0, embedding=emb)
+    print(f"embedding step: gpu {tg} oracle {to} cos {cosine(lg, lo):.7f} rel {rel_err(lg, lo):.2e}")
+    assert cosine(lg, lo) >= 0.9999 and rel_err(lg, lo) <= 2e-3 and tg == to
+    kg, _ = g.kv_read(1, 64, 2)
+    ko, _ = o.kv_read(1, 64, 2)
+    assert np.allclose(kg, ko, rtol=4e-3, atol=4e-3)
+
+
+@pytest.mark.parametrize("quant", [0, 2])
+def test_greedy_tokens_match_oracle(mdx, gpu, oracle_lib, models, quant):
+    cfg, get = models
+    path = get(quant)
+    g, o = _pair(mdx, oracle_lib, cfg, path, quant)
+    g.kv_fill_normal(300, 31)
+    assert o.kv_fill_normal(300, 31) == 0
+    toks_g, _ = g.generate_greedy(100, 16)
+    toks_o, margins = o.greedy(100, 16)
+    print(f"q{quant}: gpu {toks_g}\n    oracle {toks_o}\n    min margin {min(margins):.3g}")
+    assert list(toks_g) == list(toks_o)
+    assert g.seq_len == 316
