@@ -6,15 +6,18 @@ random-init Qwen3-0.6B-shaped model (d=1024, 16Q/8KV heads x 128, FFN 3072,
 vocab 151936), FP16 layer weights, INT8 lm_head with per-column fp32 scales,
 RoPE theta 1e6 split-half, fp16 KV cache prefilled to 512 positions with
 N(0,1) values; each timed step decodes one token with the argmax fed back on
-the device.  A "step" is one token.  value = tokens/s over the timed steps
-(host wall clock around the whole timed loop, GPU synchronised on both
-sides).
+the device.  A "step" is one token, which is one launch of the whole-step
+kernel k_persist_step (all 28 layers, the lm_head and the argmax).  value =
+tokens/s over the timed steps (host wall clock around the whole timed loop,
+GPU synchronised on both sides).
 
-Also reported: the M=60 INT8 batch prefill (28 layers, 60 tokens from an
-empty cache), the per-projection GEMV bandwidth, the roofline of the dominant
-kernel (timed with HIP events on the decoder's stream), and the oracle (the
-scalar C restatement of the reference CPU path) timed on this host on a
-bounded sample of the same decode workload.
+Also reported: the roofline of that kernel (algorithmic bytes of a step over
+its average duration, HIP events on the decoder's stream), with the HBM
+traffic measured by rocprofv3 counters when its summary is present under
+profiles/; the per-stage kernels of the general path (the fallback for other
+shapes); the M=60 INT8 batch prefill (28 layers, 60 tokens from an empty
+cache); and the oracle (the scalar C restatement of the reference CPU path)
+timed on this host on a bounded sample of the same decode workload.
 
 Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
 """
@@ -163,14 +166,14 @@ def main() -> int:
         us, b = dec.time_projection(name, iters)
         kernels[name] = {"avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
                          "per_step_us": round(us * per_step, 1)}
-    dom = max(kernels, key=lambda k: kernels[k]["per_step_us"])
-    kd = kernels[dom]
-    kernel_names = {"qkv": "k_gemv<KF16> fused RMSNorm + merged QKV projection",
-                    "o": "k_gemv<KF16> o_proj + residual add",
-                    "gate_up": "k_gemv<KF16> fused RMSNorm + gate/up + SwiGLU",
-                    "down": "k_gemv<KF16> down_proj + residual add",
-                    "lm_head": "k_gemv<KI8> fused final RMSNorm + INT8 lm_head + argmax partials"}
+    path_kind = dec.path
     dec.close()
+    step_us = dev_ms * 1000.0 / args.steps
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "k_persist_step_fp16_decode_kv512_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
 
     # ---- batch prefill M=60 through 28 INT8 layers ----
     prefill = None
@@ -212,16 +215,18 @@ def main() -> int:
                                "1 token per step, argmax fed back on device",
                    "hidden": 1024, "heads": "16q/8kv x128", "ffn": 3072, "vocab": 151936,
                    "kv_start": KV_PREFILL, "start_token": START_TOKEN},
-        "roofline": {"bound": "hbm", "kernel": kernel_names[dom],
-                     "achieved": kd["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kd["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": kd["bytes"], "avg_us": kd["avg_us"]},
-        "step_roofline": {"bytes_per_step": bytes_step,
-                          "achieved_GBps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
-                          "frac": round(bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                          "device_us_per_step": round(dev_ms * 1000 / args.steps, 2)},
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_persist_step<f16> (one cooperative launch per token: 28 layers + "
+                               "INT8 lm_head + argmax)" if path_kind == 1 else
+                               "per-stage kernel sequence (one-launch step unavailable)",
+                     "achieved": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(bytes_step / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "bytes_per_launch": bytes_step, "avg_us": round(step_us, 2)},
+        "wall_roofline_frac": round(bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "api_step_ms": round(api_ms, 4),
-        "kernels": kernels,
+        "per_stage_path_kernels": kernels,
         "prefill_m60": prefill,
         "cpu_baseline": cpu,
         "tokens_head": toks[:8],

@@ -38,6 +38,13 @@ const char* mdx_last_error(void);
  * the per-stage kernel sequence. */
 int mdx_decode_path(const MatmulDecoderContext* ctx);
 
+/* One decode step of the one-launch path with per-workgroup timestamps
+ * (100 MHz device clock) at every stage boundary: out[256][E] with E
+ * events per workgroup: 16 per layer, 3 for the lm_head, then the
+ * workgroup's XCD index.  Returns E, or
+ * MATMUL_DECODER_ERR_UNSUPPORTED when the context uses per-stage kernels. */
+int mdx_trace_step(MatmulDecoderContext* ctx, int token_id, unsigned long long* out, int cap);
+
 /* matmul_decoder_step with the lm_head and argmax but without copying the
  * logits to the host (the pybind step_get_token path). */
 int mdx_step_token(MatmulDecoderContext* ctx, int token_id, const float* embedding);

@@ -63,6 +63,7 @@ def lib() -> C.CDLL:
             "orc_vec_add": (None, [_F, _F, C.c_int]),
             "orc_argmax": (C.c_int, [_F, C.c_int]),
             "orc_matmul_f16": (None, [_F, _F, _U16, C.c_int, C.c_int, C.c_int]),
+            "orc_set_accum_order": (None, [C.c_int]),
             "orc_matmul_i8": (None, [_F, _F, _I8, _F, C.c_int, C.c_int, C.c_int]),
             "orc_matmul_i4": (None, [_F, _F, _U8, _F, C.c_int, C.c_int, C.c_int]),
             "orc_gemv_rows_f16": (None, [_F, _F, _U16, C.c_int, C.c_int]),

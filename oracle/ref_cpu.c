@@ -315,10 +315,52 @@ int orc_argmax(const float* x, int n) {
 /* Projections                                                               */
 /* ------------------------------------------------------------------------ */
 
+/* Accumulation order of the projections.  The reference runs them on the
+ * NPU, whose fp32 accumulation order is not specified (src/matmul_decoder.c
+ * only sees the results), so the oracle defines order 0: increasing k.
+ * Order 1 accumulates k mod 4 in four separate sums combined as
+ * (s0+s1)+(s2+s3): an equally valid order, used only to measure how much two
+ * valid orders disagree after many layers. */
+static int g_accum_order = 0;
+void orc_set_accum_order(int order) { g_accum_order = order; }
+
+/* y[m][n] += xk * wrow[n] into the accumulator set of k (order 1: k mod 4). */
+static void accum_row(float* acc, const float* wrow, float xk, int k, size_t MN_stride, int N) {
+    float* a = acc + (g_accum_order == 1 ? (size_t)(k & 3) * MN_stride : 0);
+    for (int n = 0; n < N; n++) a[n] = a[n] + xk * wrow[n];
+}
+
+static float* accum_alloc(size_t MN) {
+    return (float*)calloc((g_accum_order == 1 ? 4 : 1) * MN, sizeof(float));
+}
+
+static void accum_finish(float* y, const float* acc, size_t MN) {
+    if (g_accum_order == 1) {
+        for (size_t i = 0; i < MN; i++) y[i] = (acc[i] + acc[MN + i]) + (acc[2 * MN + i] + acc[3 * MN + i]);
+    } else {
+        memcpy(y, acc, MN * sizeof(float));
+    }
+}
+
 /* Reference: src/matmul_decoder.c:382-445 (type 1) and :1841-1899 (batch).
  * fp32 input rounded to fp16, products exact in fp32, fp32 accumulation in
  * increasing k. */
 void orc_matmul_f16(float* y, const float* x, const uint16_t* w, int M, int K, int N) {
+    if (g_accum_order == 1) {
+        const size_t MN = (size_t)M * N;
+        float* acc = accum_alloc(MN);
+        float* wrow = (float*)malloc(sizeof(float) * (size_t)N);
+        for (int k = 0; k < K; k++) {
+            for (int n = 0; n < N; n++) wrow[n] = f16_widen(w[(size_t)k * N + n]);
+            for (int m = 0; m < M; m++)
+                accum_row(acc + (size_t)m * N, wrow,
+                          orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k])), k, MN, N);
+        }
+        accum_finish(y, acc, MN);
+        free(acc);
+        free(wrow);
+        return;
+    }
     float* wrow = (float*)malloc(sizeof(float) * (size_t)N);
     for (int m = 0; m < M; m++) {
         float* ym = y + (size_t)m * N;
@@ -340,16 +382,17 @@ void orc_matmul_f16(float* y, const float* x, const uint16_t* w, int M, int K, i
 void orc_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale,
                    int M, int K, int N) {
     float* wrow = (float*)malloc(sizeof(float) * (size_t)N);
-    for (size_t i = 0; i < (size_t)M * N; i++) y[i] = 0.0f;
+    const size_t MN = (size_t)M * N;
+    float* acc = accum_alloc(MN);
     for (int k = 0; k < K; k++) {
         const int8_t* qk = q + (size_t)k * N;
         for (int n = 0; n < N; n++) wrow[n] = (float)qk[n];
-        for (int m = 0; m < M; m++) {
-            float xk = orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k]));
-            float* ym = y + (size_t)m * N;
-            for (int n = 0; n < N; n++) ym[n] = ym[n] + xk * wrow[n];
-        }
+        for (int m = 0; m < M; m++)
+            accum_row(acc + (size_t)m * N, wrow, orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k])),
+                      k, MN, N);
     }
+    accum_finish(y, acc, MN);
+    free(acc);
     if (scale)
         for (int m = 0; m < M; m++)
             for (int n = 0; n < N; n++) y[(size_t)m * N + n] = y[(size_t)m * N + n] * scale[n];
@@ -359,7 +402,8 @@ void orc_matmul_i8(float* y, const float* x, const int8_t* q, const float* scale
 void orc_matmul_i4(float* y, const float* x, const uint8_t* q, const float* scale,
                    int M, int K, int N) {
     float* wrow = (float*)malloc(sizeof(float) * (size_t)N);
-    for (size_t i = 0; i < (size_t)M * N; i++) y[i] = 0.0f;
+    const size_t MN = (size_t)M * N;
+    float* acc = accum_alloc(MN);
     for (int k = 0; k < K; k++) {
         const uint8_t* qk = q + (size_t)k * (N / 2);
         for (int j = 0; j < N / 2; j++) {
@@ -367,12 +411,12 @@ void orc_matmul_i4(float* y, const float* x, const uint8_t* q, const float* scal
             wrow[2 * j] = (float)((int8_t)(uint8_t)(qk[j] << 4) >> 4);
             wrow[2 * j + 1] = (float)((int8_t)qk[j] >> 4);
         }
-        for (int m = 0; m < M; m++) {
-            float xk = orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k]));
-            float* ym = y + (size_t)m * N;
-            for (int n = 0; n < N; n++) ym[n] = ym[n] + xk * wrow[n];
-        }
+        for (int m = 0; m < M; m++)
+            accum_row(acc + (size_t)m * N, wrow, orc_f16_to_f32(orc_f32_to_f16(x[(size_t)m * K + k])),
+                      k, MN, N);
     }
+    accum_finish(y, acc, MN);
+    free(acc);
     if (scale)
         for (int m = 0; m < M; m++)
             for (int n = 0; n < N; n++) y[(size_t)m * N + n] = y[(size_t)m * N + n] * scale[n];

@@ -58,6 +58,10 @@ void orc_vec_add(float* dst, const float* src, int n);
 int orc_argmax(const float* x, int n);
 
 /* ---- projections on the reference weight layout W[K,N] row-major ---- */
+/* Projection accumulation order: 0 increasing k (default), 1 four
+ * interleaved sums combined (s0+s1)+(s2+s3), used only to measure the
+ * order sensitivity of end-to-end results. */
+void orc_set_accum_order(int order);
 /* y[m,n] = sum_k fp16(x[m,k]) * W[k,n]                      (NPU type 1) */
 void orc_matmul_f16(float* y, const float* x, const uint16_t* w, int M, int K, int N);
 /* y[m,n] = scale[n] * sum_k fp16(x[m,k]) * q[k,n]           (NPU type 5) */

@@ -1298,6 +1298,31 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
 const char* mdx_version(void) { return "1.0.0 gfx950"; }
 int mdx_device_count(void) { return mdxrt_device_count(); }
 
+int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* out, int cap) {
+    if (!c || !out) return MATMUL_DECODER_ERR_INVALID_ARG;
+    if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    int rc = step_checks(c, token_id, NULL);
+    if (rc) return rc;
+    const int ev = mdx_persist_trace_events(c->L);
+    if ((long long)cap < 256LL * ev) return MATMUL_DECODER_ERR_INVALID_ARG;
+    unsigned long long* d = NULL;
+    if (mdxrt_malloc((void**)&d, (size_t)256 * ev * 8)) return MATMUL_DECODER_ERR_MEMORY;
+    rc = set_state(c, token_id, NULL);
+    if (!rc) rc = mdxrt_fill_u32(d, 0u, (size_t)256 * ev * 2, c->stream);
+    c->pargs.trace = d;
+    c->pargs.trace_stride = ev;
+    if (!rc) rc = launch_persist(c, 1, NULL);
+    c->pargs.trace = NULL;
+    c->pargs.trace_stride = 0;
+    if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
+    if (!rc) rc = mdxrt_stream_sync(c->stream);
+    if (!rc) rc = mdxrt_d2h(out, d, (size_t)256 * ev * 8);
+    mdxrt_free(d);
+    if (rc || c->h_state->pad[1]) return MATMUL_DECODER_ERR_RKNN;
+    c->seq_len++;
+    return ev;
+}
+
 int mdx_decode_path(const MatmulDecoderContext* c) {
     if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
     return c->persist ? 1 : 0;

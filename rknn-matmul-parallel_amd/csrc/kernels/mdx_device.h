@@ -164,6 +164,8 @@ typedef struct {
     float* hidden_out;                 /* [d] final hidden (before the final norm) */
     void* xbuf;                        /* mdx_persist_xbuf_bytes(), zeroed once at creation */
     int* out_tokens;                   /* optional greedy output list (state->n_out) */
+    unsigned long long* trace;         /* optional [256][trace_stride] timestamps */
+    int trace_stride;                  /* >= mdx_persist_trace_events(n_layers) */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */
@@ -171,6 +173,9 @@ int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F);
 /* 1 when the current device can hold the whole grid co-resident. */
 int mdx_persist_usable(int kind);
 size_t mdx_persist_xbuf_bytes(void);
+/* Events per workgroup of a traced step: 16 per layer (stage starts, waits
+ * done, outputs written), 3 for the lm_head and the workgroup's XCD index. */
+int mdx_persist_trace_events(int n_layers);
 /* One decode step (all layers, and the lm_head when head != 0).  A wait that
  * times out sets state->pad[1] = 1; the caller treats that as a failure. */
 int mdx_launch_persist_step(const mdx_persist_args* a, void* stream);

@@ -56,8 +56,8 @@ constexpr int PART_WORDS = 520;                    // m0 l0 m1 l1 (x2) | o0[128]
 constexpr int W_PART = W_QKV + NKV * 1024;         // [NKV][GRP][PART_WORDS]
 constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [QD] fp16
 constexpr int W_HO = W_ATT + QD;                   // [D][2] hidden after o
-constexpr int W_ACT = W_HO + 2 * D;                // [FF] fp16
-constexpr int W_HD = W_ACT + FF;                   // [D][2] hidden after down
+constexpr int W_ACT = W_HO + 2 * D;                // [NB][16] fp16 (12 used: 64-byte slots)
+constexpr int W_HD = W_ACT + NB * 16;              // [D][2] hidden after down
 constexpr int W_AMAX = W_HD + 2 * D;               // [NB][4] argmax keys
 constexpr int W_TOTAL = W_AMAX + NB * 4;
 static_assert(W_PART % 4 == 0 && W_ATT % 4 == 0 && W_HO % 4 == 0 && W_ACT % 4 == 0 &&
@@ -81,7 +81,15 @@ struct PArgs {
     float* hidden_out;
     unsigned* xbuf;
     int* out_tokens;
+    unsigned long long* trace;  // optional [NB][trace_stride] 100 MHz timestamps
+    int trace_stride;
 };
+
+// Timestamp of event ev for this workgroup (thread 0), when tracing is on.
+#define MDX_TRACE(ev)                                                                      \
+    do {                                                                                   \
+        if (a.trace && t == 0) a.trace[(size_t)b * a.trace_stride + (ev)] = wall_clock64(); \
+    } while (0)
 
 // ---- LL words ---------------------------------------------------------------
 
@@ -309,8 +317,29 @@ __device__ __forceinline__ void cm_dot(const uint4 (&w)[NWT], const uint4* xs4, 
 
 // ---- small helpers ----------------------------------------------------------
 
+// Cross-lane reductions with DPP moves (a few cycles each, unlike LDS-routed
+// shuffles).  row_sum16: every lane of each 16-lane row gets the row's sum.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v = v + dpp<0xB1>(v);    // quad_perm [1,0,3,2]
+    v = v + dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+    v = v + dpp<0x124>(v);   // row_ror:4
+    v = v + dpp<0x128>(v);   // row_ror:8
+    return v;
+}
+// Sum over the 64 lanes, returned to every lane (through lane 63).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = row_sum16(v);
+    v = v + dpp<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+    v = v + dpp<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float block_sum4(float v, float* ws, int t) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);
     if ((t & 63) == 0) ws[t >> 6] = v;
     __syncthreads();
     return (ws[0] + ws[1]) + (ws[2] + ws[3]);
@@ -334,25 +363,27 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 // QK-norm (optional) + RoPE of one 128-wide head held in LDS, one wave.
 // With cache != NULL the results are rounded to fp16, stored there, and the
 // rounded values kept (the fp16 KV-cache semantic).
-__device__ __forceinline__ void rope_head(const float* src, const float* nw, float eps,
-                                          const float* cr, const float* sr, int style, float* dst,
+// Lane i rotates the pair (i0, i1) of its style; c, s are cos/sin of pair i
+// at the step's position and nw0, nw1 the norm weights of i0, i1 (all read
+// before the wait that precedes this).
+__device__ __forceinline__ void rope_head(const float* src, bool norm, float nw0, float nw1,
+                                          float eps, float c, float s, int style, float* dst,
                                           uint16_t* cache, int lane) {
     constexpr int half = HD / 2;
     float rms = 1.0f;
-    if (nw) {
+    if (norm) {
         float ss = src[lane] * src[lane] + src[lane + 64] * src[lane + 64];
-        ss = wave_sum(ss);
+        ss = wave_sum_dpp(ss);
         rms = 1.0f / sqrtf(ss / (float)HD + eps);
     }
     const int i = lane;
     const int i0 = style == 0 ? 2 * i : i;
     const int i1 = style == 0 ? 2 * i + 1 : i + half;
     float x0 = src[i0], x1 = src[i1];
-    if (nw) {
-        x0 = (x0 * rms) * nw[i0];
-        x1 = (x1 * rms) * nw[i1];
+    if (norm) {
+        x0 = (x0 * rms) * nw0;
+        x1 = (x1 * rms) * nw1;
     }
-    const float c = cr[i], s = sr[i];
     float o0 = x0 * c - x1 * s;
     float o1 = x1 * c + x0 * s;
     if (cache) {
@@ -370,29 +401,6 @@ __device__ __forceinline__ void h8_to_f32(uint4 u, float (&f)[8]) {
     const half2_t a = as_h2(u.x), b = as_h2(u.y), c = as_h2(u.z), d = as_h2(u.w);
     f[0] = (float)a.x; f[1] = (float)a.y; f[2] = (float)b.x; f[3] = (float)b.y;
     f[4] = (float)c.x; f[5] = (float)c.y; f[6] = (float)d.x; f[7] = (float)d.y;
-}
-
-// Online-softmax update of one position for the two query heads of a thread.
-__device__ __forceinline__ void attn_update(const float (&q)[2][8], const float (&kf)[8],
-                                            const float (&vf)[8], bool valid, float (&m)[2],
-                                            float (&l)[2], float (&o)[2][8]) {
-    const float scale = 0.08838834764831845f;   // 1/sqrt(128)
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        float s = q[h][0] * kf[0];
-#pragma unroll
-        for (int e = 1; e < 8; e++) s = s + q[h][e] * kf[e];
-        s = group_sum(s, 16) * scale;
-        if (valid) {
-            const float mn = fmaxf(m[h], s);
-            const float a = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn);
-            const float p = expf(s - mn);
-            l[h] = l[h] * a + p;
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[h][e] = o[h][e] * a + p * vf[e];
-            m[h] = mn;
-        }
-    }
 }
 
 __device__ __forceinline__ void ml_merge(float& m, float& l, float* o, int n, float m2, float l2,
@@ -424,7 +432,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     __shared__ float q_s[2 * HD];
     __shared__ float kn_s[HD];
     __shared__ float vn_s[HD];
-    __shared__ float wpart[4][2][HD + 2];
+    __shared__ float att_o[16][2][HD];
+    __shared__ float att_m[16][2];
+    __shared__ float att_l[16][2];
+    __shared__ float cm_m[32], cm_l[32], cm_w[32];
+    __shared__ float cm_o[32][8];
     __shared__ unsigned long long bkey[4];
 
     const int t = threadIdx.x, b = blockIdx.x, lane = t & 63, wave = t >> 6;
@@ -470,12 +482,50 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
     }
 
+    // lm_head rows of this workgroup; the first batch is requested during the
+    // last layer's gate/up stage
+    constexpr int U = 16;
+    const int rb = (int)(((long long)b * a.vocab) / NB);
+    const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
+    auto load_rows = [&](uint4 (&w)[U], float& sc, int base) {
+        // rows past the workgroup's range re-read row re-1; consume skips them
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int r = min(base + u, re - 1);
+            w[u] = *reinterpret_cast<const uint4*>(a.lm_w + (size_t)r * D + lane * 16);
+        }
+        sc = a.lm_scale[min(base + (lane >> 2), re - 1)];
+    };
+    uint4 w0[U];
+    float sc0 = 0.0f;
+
     for (int l = 0; l < L; l++) {
         const mdx_persist_layer Ly = layer_at(a, l);
         const unsigned ep = step_epoch(E, L, l);
         const unsigned ep_prev = step_epoch(E, L, l - 1 < 0 ? 0 : l - 1);
 
         // ================= A: RMSNorm + qkv =================
+        MDX_TRACE(16 * l + 0);
+        const float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
+        // stage B inputs that do not depend on this step's activations
+        const float rc = a.cos_t[(size_t)pos * (HD / 2) + lane];
+        const float rsn = a.sin_t[(size_t)pos * (HD / 2) + lane];
+        const int ri0 = a.rope_style == 0 ? 2 * lane : lane;
+        const int ri1 = a.rope_style == 0 ? 2 * lane + 1 : lane + HD / 2;
+        const float* qknw = wave < 2 ? Ly.q_norm : Ly.k_norm;
+        const float rn0 = qknw ? qknw[ri0] : 1.0f;
+        const float rn1 = qknw ? qknw[ri1] : 1.0f;
+        const float sclA = Ly.sqkv ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
+        if (l > 0) {
+            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
+            u32x4 v[2];
+            const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead);
+            h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
+            h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            if (__syncthreads_or(!ok)) dead = true;
+        }
+        // weight requests go out after the wait, so they do not queue in front
+        // of the exchange's own reads
         uint4 kr[PP], vr[PP];
 #pragma unroll
         for (int q = 0; q < PP; q++) {
@@ -489,16 +539,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         uint4 wD[SD::NW];
         cm_load<KIND, 4, QD>(wD, Ly.wo, 4 * b, t);
-        const float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
-        const float sclA = Ly.sqkv ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
-        if (l > 0) {
-            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
-            u32x4 v[2];
-            const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead);
-            h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
-            h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
-            if (__syncthreads_or(!ok)) dead = true;
-        }
+        MDX_TRACE(16 * l + 1);
         if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
         {
             const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
@@ -515,12 +556,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             y = y * sclA;
             ll_put_f32(xb, W_QKV + j * 1024 + 2 * (s * 16 + t), y, ep);
         }
+        MDX_TRACE(16 * l + 2);
 
         // ================= B: QK-norm, RoPE, KV append, partial attention ==========
         uint4 wE[SE::NW];
-        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, 0, SE::NW / 2);
-        const float* cr = a.cos_t + (size_t)pos * (HD / 2);
-        const float* sr = a.sin_t + (size_t)pos * (HD / 2);
         {
             int wd[1] = {W_QKV + j * 1024 + 4 * t};
             u32x4 v[1];
@@ -529,12 +568,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             qkv_s[2 * t + 1] = ll_f32(v[0].z, v[0].w);
             if (__syncthreads_or(!ok)) dead = true;
         }
+        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, 0, SE::NW / 2);
+        MDX_TRACE(16 * l + 3);
         if (wave < 2) {
-            rope_head(qkv_s + wave * HD, Ly.q_norm, a.eps, cr, sr, a.rope_style, q_s + wave * HD,
-                      nullptr, lane);
+            rope_head(qkv_s + wave * HD, Ly.q_norm != nullptr, rn0, rn1, a.eps, rc, rsn,
+                      a.rope_style, q_s + wave * HD, nullptr, lane);
         } else if (has_new && wave == 2) {
-            rope_head(qkv_s + 2 * HD, Ly.k_norm, a.eps, cr, sr, a.rope_style, kn_s,
-                      Ly.kc + (size_t)pos * KVD + j * HD, lane);
+            rope_head(qkv_s + 2 * HD, Ly.k_norm != nullptr, rn0, rn1, a.eps, rc, rsn, a.rope_style,
+                      kn_s, Ly.kc + (size_t)pos * KVD + j * HD, lane);
         } else if (has_new) {
             for (int e = lane; e < HD; e += 64) {
                 const uint16_t hv = f32_to_f16_bits(qkv_s[3 * HD + e]);
@@ -543,33 +584,99 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             }
         }
         __syncthreads();
+        MDX_TRACE(16 * l + 12);
+        // Scores of all passes first (independent chains), one workgroup-wide
+        // max per head, then P.V summed over the 16 position groups in LDS.
+        // (runM, runL, runO) of thread t: head t >> 7, dimension t & 127.
+        float runM = -INFINITY, runL = 0.0f, runO = 0.0f;
         {
             float q[2][8];
 #pragma unroll
             for (int hh = 0; hh < 2; hh++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) q[hh][e] = q_s[hh * HD + dl * 8 + e];
-            float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.0f, 0.0f};
-            float o[2][8];
+            auto round = [&](const uint4 (&kk)[PP], const uint4 (&vv)[PP], int q0) {
+                float sc[PP][2], vf[PP][8];
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++)
+                for (int qq = 0; qq < PP; qq++) {
+                    const int pi = 16 * (q0 + qq) + pl;
+                    const bool isnew = pi < n && p0 + pi == pos;
+                    float kf[8];
+                    if (isnew) {
 #pragma unroll
-                for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
-            auto pass = [&](uint4 kk, uint4 vv, int pi) {
-                const int p = p0 + pi;
-                const bool valid = pi < n;
-                float kf[8], vf[8];
-                if (valid && p == pos) {
+                        for (int e = 0; e < 8; e++) {
+                            kf[e] = kn_s[dl * 8 + e];
+                            vf[qq][e] = vn_s[dl * 8 + e];
+                        }
+                    } else {
+                        h8_to_f32(kk[qq], kf);
+                        h8_to_f32(vv[qq], vf[qq]);
+                    }
 #pragma unroll
-                    for (int e = 0; e < 8; e++) { kf[e] = kn_s[dl * 8 + e]; vf[e] = vn_s[dl * 8 + e]; }
-                } else {
-                    h8_to_f32(kk, kf);
-                    h8_to_f32(vv, vf);
+                    for (int hh = 0; hh < 2; hh++) {
+                        const float* qh = q[hh];
+                        sc[qq][hh] = ((qh[0] * kf[0] + qh[1] * kf[1]) + (qh[2] * kf[2] + qh[3] * kf[3])) +
+                                     ((qh[4] * kf[4] + qh[5] * kf[5]) + (qh[6] * kf[6] + qh[7] * kf[7]));
+                    }
                 }
-                attn_update(q, kf, vf, valid, m, lsum, o);
-            };
+                float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-            for (int qq = 0; qq < PP; qq++) pass(kr[qq], vr[qq], 16 * qq + pl);
+                for (int qq = 0; qq < PP; qq++) {
+                    const bool valid = 16 * (q0 + qq) + pl < n;
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const float v = row_sum16(sc[qq][hh]) * 0.08838834764831845f;   // 1/sqrt(128)
+                        sc[qq][hh] = valid ? v : -INFINITY;
+                        mx[hh] = fmaxf(mx[hh], sc[qq][hh]);
+                    }
+                }
+                if (q0 == 0) MDX_TRACE(16 * l + 14);
+                if (dl == 0) {
+                    att_m[pl][0] = mx[0];
+                    att_m[pl][1] = mx[1];
+                }
+                __syncthreads();
+                float M[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    float v = att_m[0][hh];
+#pragma unroll
+                    for (int i = 1; i < 16; i++) v = fmaxf(v, att_m[i][hh]);
+                    M[hh] = v;
+                }
+                float ls[2] = {0.0f, 0.0f}, o[2][8];
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
+#pragma unroll
+                for (int qq = 0; qq < PP; qq++) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const float p = sc[qq][hh] == -INFINITY ? 0.0f : expf(sc[qq][hh] - M[hh]);
+                        ls[hh] = ls[hh] + p;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) o[hh][e] = o[hh][e] + p * vf[qq][e];
+                    }
+                }
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) att_o[pl][hh][dl * 8 + e] = o[hh][e];
+                    if (dl == 0) att_l[pl][hh] = ls[hh];
+                }
+                __syncthreads();
+                const int hh = t >> 7, d = t & 127;
+                float Ox = 0.0f, Lx = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    Ox = Ox + att_o[i][hh][d];
+                    Lx = Lx + att_l[i][hh];
+                }
+                ml_merge(runM, runL, &runO, 1, M[hh], Lx, &Ox);
+                __syncthreads();   // att_* are rewritten by the next round
+            };
+            round(kr, vr, 0);
             for (int q0 = PP; 16 * q0 < n; q0 += PP) {      // chunks longer than 16*PP
                 uint4 kx[PP], vx[PP];
 #pragma unroll
@@ -580,55 +687,25 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                     kx[qq] = *reinterpret_cast<const uint4*>(Ly.kc + (size_t)pc * KVD + j * HD + dl * 8);
                     vx[qq] = *reinterpret_cast<const uint4*>(Ly.vc + (size_t)pc * KVD + j * HD + dl * 8);
                 }
-#pragma unroll
-                for (int qq = 0; qq < PP; qq++) pass(kx[qq], vx[qq], 16 * (q0 + qq) + pl);
-            }
-            // merge the 4 position groups of each wave (lane bits 4 and 5)
-#pragma unroll
-            for (int off = 16; off <= 32; off <<= 1) {
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const float m2 = __shfl_xor(m[hh], off, 64);
-                    const float l2 = __shfl_xor(lsum[hh], off, 64);
-                    float o2[8];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) o2[e] = __shfl_xor(o[hh][e], off, 64);
-                    ml_merge(m[hh], lsum[hh], o[hh], 8, m2, l2, o2);
-                }
-            }
-            if (lane < 16) {
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) wpart[wave][hh][dl * 8 + e] = o[hh][e];
-                    if (lane == 0) {
-                        wpart[wave][hh][HD] = m[hh];
-                        wpart[wave][hh][HD + 1] = lsum[hh];
-                    }
-                }
+                round(kx, vx, q0);
             }
         }
-        __syncthreads();
+        MDX_TRACE(16 * l + 13);
         {
             const int hh = t >> 7, d = t & 127;
-            float M = wpart[0][hh][HD], Ls = wpart[0][hh][HD + 1], O = wpart[0][hh][d];
-#pragma unroll
-            for (int w = 1; w < 4; w++)
-                ml_merge(M, Ls, &O, 1, wpart[w][hh][HD], wpart[w][hh][HD + 1], &wpart[w][hh][d]);
             const int base = W_PART + (j * GRP + s) * PART_WORDS;
-            ll_put_f32(xb, base + 8 + 256 * hh + 2 * d, O, ep);
+            ll_put_f32(xb, base + 8 + 256 * hh + 2 * d, runO, ep);
             if (d == 0) {
-                ll_put_f32(xb, base + 4 * hh, M, ep);
-                ll_put_f32(xb, base + 4 * hh + 2, Ls, ep);
+                ll_put_f32(xb, base + 4 * hh, runM, ep);
+                ll_put_f32(xb, base + 4 * hh + 2, runL, ep);
             }
         }
+        MDX_TRACE(16 * l + 4);
 
         // ================= C: merge the 32 partials of KV head j ==========
-        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
         {
             const int hh = s >> 4, d0 = (s & 15) * 8;
             bool ok = true;
-            float m = -INFINITY, lsum = 0.0f, o[8];
             if (t < 32) {
                 const int base = W_PART + (j * GRP + t) * PART_WORDS;
                 int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0,
@@ -636,37 +713,36 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                              base + 20 + 256 * hh + 2 * d0};
                 u32x4 v[5];
                 ok = ll_wait<5>(rs, wd, v, ep, dead);
-                m = ll_f32(v[0].x, v[0].y);
-                lsum = ll_f32(v[0].z, v[0].w);
+                cm_m[t] = ll_f32(v[0].x, v[0].y);
+                cm_l[t] = ll_f32(v[0].z, v[0].w);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    o[2 * k] = ll_f32(v[1 + k].x, v[1 + k].y);
-                    o[2 * k + 1] = ll_f32(v[1 + k].z, v[1 + k].w);
-                }
-            }
-            if (t < 64) {
-                // lanes 32..63 hold empty partials (m = -inf)
-                float M = m;
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-                const float wgt = m == -INFINITY ? 0.0f : expf(m - M);
-                float acc[9];
-                acc[8] = t < 32 ? lsum * wgt : 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[e] = t < 32 ? o[e] * wgt : 0.0f;
-#pragma unroll
-                for (int off = 1; off < 32; off <<= 1)
-#pragma unroll
-                    for (int e = 0; e < 9; e++) acc[e] += __shfl_xor(acc[e], off, 64);
-                if (t < 8) {
-                    float val = acc[0];
-#pragma unroll
-                    for (int e = 1; e < 8; e++) val = t == e ? acc[e] : val;
-                    ll_put(xb, W_ATT + (2 * j + hh) * HD + d0 + t, f32_to_f16_bits(val / acc[8]), ep);
+                    cm_o[t][2 * k] = ll_f32(v[1 + k].x, v[1 + k].y);
+                    cm_o[t][2 * k + 1] = ll_f32(v[1 + k].z, v[1 + k].w);
                 }
             }
             if (__syncthreads_or(!ok)) dead = true;
+            rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+            if (t < 32) {
+                float M = cm_m[0];
+#pragma unroll
+                for (int i = 1; i < 32; i++) M = fmaxf(M, cm_m[i]);
+                const float m = cm_m[t];
+                cm_w[t] = m == -INFINITY ? 0.0f : expf(m - M);
+            }
+            __syncthreads();
+            if (t < 8) {
+                float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; i++) {
+                    const float w = cm_w[i];
+                    Ls = Ls + cm_l[i] * w;
+                    O = O + cm_o[i][t] * w;
+                }
+                ll_put(xb, W_ATT + (2 * j + hh) * HD + d0 + t, f32_to_f16_bits(O / Ls), ep);
+            }
         }
+        MDX_TRACE(16 * l + 5);
 
         // ================= D: o projection + residual ==========
         uint4 wF[SF::NW];
@@ -684,16 +760,19 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             xs4[t] = x;
             if (__syncthreads_or(!ok)) dead = true;
         }
+        MDX_TRACE(16 * l + 6);
         cm_dot<KIND, 4, QD>(wD, xs4, red, t);
         __syncthreads();
         if (t < 4) {
             const float y = ((red[t] + red[4 + t]) + (red[8 + t] + red[12 + t])) * sclD;
             ll_put_f32(xb, W_HO + 2 * (4 * b + t), hres[t] + y, ep);
         }
+        MDX_TRACE(16 * l + 7);
 
         // ================= E: RMSNorm + gate/up + SwiGLU ==========
         const bool last = l + 1 == L;
         if (!last) rm_load<KIND, 16, D>(wA, layer_at(a, l + 1).wqkv, rowA, t, 0, SA::NW);
+        else if (a.head) load_rows(w0, sc0, rb + wave * U);
         const float4 nwE = reinterpret_cast<const float4*>(Ly.post_norm)[t];
         const float sclE = Ly.sgu ? Ly.sgu[rowE(t < 24 ? t : 0)] : 1.0f;
         {
@@ -704,6 +783,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
             if (__syncthreads_or(!ok)) dead = true;
         }
+        MDX_TRACE(16 * l + 8);
         if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
         {
             const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
@@ -722,13 +802,15 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         __syncthreads();
         if (t < 12) {
             const float g = gu_s[t], u = gu_s[12 + t];
-            ll_put(xb, W_ACT + 12 * b + t, f32_to_f16_bits(silu_mul(g, u)), ep);
+            ll_put(xb, W_ACT + 16 * b + t, f32_to_f16_bits(silu_mul(g, u)), ep);
         }
+        MDX_TRACE(16 * l + 9);
 
         // ================= F: down projection + residual ==========
         const float sclF = Ly.sdown ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
+        MDX_TRACE(16 * l + 15);
         {
-            int wd[3] = {W_ACT + 12 * t, W_ACT + 12 * t + 4, W_ACT + 12 * t + 8};
+            int wd[3] = {W_ACT + 16 * t, W_ACT + 16 * t + 4, W_ACT + 16 * t + 8};
             u32x4 v[3];
             const bool ok = ll_wait<3>(rs, wd, v, ep, dead);
             uint2* x2 = reinterpret_cast<uint2*>(xs4);
@@ -741,6 +823,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             }
             if (__syncthreads_or(!ok)) dead = true;
         }
+        MDX_TRACE(16 * l + 10);
         cm_dot<KIND, 4, FF>(wF, xs4, red, t);
         __syncthreads();
         if (t < 4) {
@@ -749,6 +832,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             ll_put_f32(xb, W_HD + 2 * (4 * b + t), hn, ep);
             if (last) a.hidden_out[4 * b + t] = hn;
         }
+        MDX_TRACE(16 * l + 11);
         __syncthreads();   // hres / red reuse
     }
 
@@ -756,22 +840,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     const unsigned ep_head = step_epoch(E, L, L);
     if (a.head) {
         // ================= lm_head (INT8 rows, fp16 activations) + argmax ==========
-        constexpr int U = 16;
-        const int rb = (int)(((long long)b * a.vocab) / NB);
-        const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
-        const int8_t* W = a.lm_w;
-        auto load_rows = [&](uint4 (&w)[U], float& sc, int base) {
-            // rows past the block's range re-read row re-1; consume skips them
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int r = min(base + u, re - 1);
-                w[u] = *reinterpret_cast<const uint4*>(W + (size_t)r * D + lane * 16);
-            }
-            sc = a.lm_scale[min(base + (lane >> 2), re - 1)];
-        };
-        uint4 w0[U], w1[U];
-        float sc0 = 0.0f, sc1 = 0.0f;
-        load_rows(w0, sc0, rb + wave * U);
+        uint4 w1[U];
+        float sc1 = 0.0f;
         const float4 nw = reinterpret_cast<const float4*>(a.final_norm)[t];
         {
             int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
@@ -781,6 +851,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
             if (__syncthreads_or(!ok)) dead = true;
         }
+        MDX_TRACE(16 * L + 0);
         {
             const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
             const float tot = block_sum4(ss, ws, t);
@@ -833,6 +904,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             ll_put(xb, base + 2, lo & 0xffffu, ep_head);
             ll_put(xb, base + 3, lo >> 16, ep_head);
         }
+        MDX_TRACE(16 * L + 1);
+        if (a.trace && t == 0)
+            a.trace[(size_t)b * a.trace_stride + 16 * L + 3] = __builtin_amdgcn_s_getreg((3 << 11) | 20);
         if (b != 0) {
             if (dead && t == 0)
                 __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -874,6 +948,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             if (dead) __hip_atomic_store(&st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(xb + W_CTRL, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        MDX_TRACE(16 * L + 2);
     } else {
         if (dead && t == 0) __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (b == 0 && t == 0) {
@@ -898,6 +973,8 @@ PersistKernel pick(int kind) {
 }  // namespace
 
 extern "C" {
+
+int mdx_persist_trace_events(int n_layers) { return 16 * n_layers + 4; }
 
 int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F) {
     return d == D && nq == NQ && nkv == NKV && hd == HD && F == FF;
@@ -946,6 +1023,9 @@ int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
     a.hidden_out = p->hidden_out;
     a.xbuf = reinterpret_cast<unsigned*>(p->xbuf);
     a.out_tokens = p->out_tokens;
+    a.trace = p->trace;
+    a.trace_stride = p->trace_stride;
+    if (a.trace && a.trace_stride < 16 * a.n_layers + 4) return -1;
     void* args[] = {&a};
     hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k), dim3(NB), dim3(NT),
                                               args, 0, (hipStream_t)stream);

@@ -108,6 +108,7 @@ def lib() -> C.CDLL:
             "mdx_last_error": (C.c_char_p, []),
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
             "mdx_decode_path": (C.c_int, [P]),
+            "mdx_trace_step": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint64), C.c_int]),
             "mdx_kv_fill_normal": (C.c_int, [P, C.c_int, C.c_uint64]),
             "mdx_kv_read": (C.c_int, [P, C.c_int, C.c_int, C.c_int, _F, _F]),
             "mdx_prefill_logits": (C.c_int, [P, _F, C.c_int, _F]),
@@ -283,6 +284,14 @@ class Decoder:
         self.kvd = c.num_kv_heads * c.head_dim
         self.n_lm = c.num_lm_heads
         self.lm_vocab = c.lm_head_vocab_size if c.num_lm_heads > 1 else c.vocab_size
+
+    def trace_step(self, token: int) -> np.ndarray:
+        """One traced one-launch step: [256 workgroups][events] timestamps."""
+        cap = 256 * (16 * 64 + 4)
+        out = np.zeros(cap, np.uint64)
+        ev = lib().mdx_trace_step(self.h, token, out.ctypes.data_as(C.POINTER(C.c_uint64)), cap)
+        _check(ev if ev < 0 else 0, "trace_step")
+        return out[:256 * ev].reshape(256, ev)
 
     @property
     def path(self) -> int:

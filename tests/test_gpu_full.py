@@ -2,12 +2,25 @@
 FFN 3072, vocab 151936, INT8 lm_head, split-half RoPE theta 1e6):
 
 - 28-layer greedy decode, FP16 layers, fp16 KV prefilled to 512 N(0,1)
-  positions, 64 greedy steps: tokens identical to the oracle, first-step
-  logits cosine >= 0.9999;
+  positions, 64 greedy steps;
 - M=60 batch prefill through 28 INT8 layers from an empty cache, then the
   lm_head on the last token: cosine >= 0.9999, same argmax;
-- W4A16 decode at long context (KV 4096, max_seq 4224), 128 greedy steps:
-  tokens identical.
+- W4A16 decode at long context (KV 4096, max_seq 4224), 128 greedy steps.
+
+Greedy parity.  The reference runs the projections on an NPU whose fp32
+accumulation order is unspecified, so the oracle fixes one order (increasing
+k).  A second, equally valid order (four interleaved sums, the oracle's
+order 1) already moves the step-0 logits by about 2e-3 of their range and
+makes the two oracle runs pick different tokens wherever the top-2 margin
+is that small (with random-init weights this happens within 64 steps).
+The decode tests therefore measure that order sensitivity B (max |logit
+difference| between the oracle's two orders at step 0) and require:
+  1. the GPU's step-0 logits within 2*B of the oracle's, cosine >= 0.9999;
+  2. teacher forcing (both fed the oracle's tokens): the GPU argmax equals
+     the oracle's at every step whose oracle top-1/top-2 margin is >= 2*B,
+     and is one of the oracle's candidates within 2*B of the top otherwise;
+  3. free-running greedy tokens identical to the oracle's up to the first
+     step whose margin is below 2*B (all of them when there is none).
 
 Model files are written at test time by the seeded synthetic writer (seed
 1000 + config number)."""
@@ -48,25 +61,74 @@ def _first_divergence(a, b):
     return None
 
 
-def test_decode_28_layers_fp16_tokens_match_oracle(mdx, gpu, oracle_lib, full):
+def _order_sensitivity(oracle_lib, path, quant, max_seq, n_pos, seed):
+    """Max |logit difference| at the first step between the oracle's two
+    projection accumulation orders, and the order-0 logits."""
+    out = []
+    for order in (0, 1):
+        oracle_lib.lib().orc_set_accum_order(order)
+        try:
+            m = oracle_lib.Model(path, FULL, quant, max_seq, kv_fp16=True)
+            assert m.kv_fill_normal(n_pos, seed) == 0
+            out.append(m.step(START)[1])
+            m.close()
+        finally:
+            oracle_lib.lib().orc_set_accum_order(0)
+    return float(np.max(np.abs(out[0] - out[1]))), out[0]
+
+
+def _greedy_parity(mdx, oracle_lib, g, o, path, quant, max_seq, n_pos, seed, n_steps):
+    bound, lo0 = _order_sensitivity(oracle_lib, path, quant, max_seq, n_pos, seed)
+    delta = 2.0 * bound
+    # oracle free-running greedy: tokens, logits and margins
+    assert o.kv_fill_normal(n_pos, seed) == 0
+    toks_o, logits_o, margins = [], [], []
+    t = START
+    for _ in range(n_steps):
+        t, lg = o.step(t)
+        top2 = np.partition(lg, -2)[-2:]
+        toks_o.append(int(t))
+        logits_o.append(lg)
+        margins.append(float(top2[1] - top2[0]))
+    assert np.array_equal(logits_o[0], lo0)
+    # GPU teacher-forced on the oracle's inputs
+    g.kv_fill_normal(n_pos, seed)
+    inputs = [START] + toks_o[:-1]
+    worst_cos, errs, near = 1.0, [], 0
+    for i, tok_in in enumerate(inputs):
+        tg, lg = g.step(tok_in)
+        lo = logits_o[i]
+        errs.append(float(np.max(np.abs(lg - lo))))
+        worst_cos = min(worst_cos, cosine(lg, lo))
+        if margins[i] >= delta:
+            assert tg == toks_o[i], (f"step {i}: gpu {tg} oracle {toks_o[i]} margin {margins[i]:.3g} "
+                                     f">= {delta:.3g}")
+        else:
+            near += 1
+            assert lo[tg] >= lo.max() - delta, f"step {i}: gpu {tg} is not an oracle near-tie candidate"
+    # GPU free-running
+    g.kv_fill_normal(n_pos, seed)
+    toks_g, _ = g.generate_greedy(START, n_steps)
+    first_tie = next((i for i, m in enumerate(margins) if m < delta), None)
+    div = _first_divergence(toks_g, toks_o)
+    print(f"order sensitivity B {bound:.3g}; gpu step-0 error {errs[0]:.3g} (max {max(errs):.3g}); "
+          f"worst cos {worst_cos:.7f}; near-tie steps {near}/{n_steps}; first near tie {first_tie}; "
+          f"first free-running divergence {div}")
+    assert errs[0] <= 2.0 * bound and worst_cos >= 0.9999
+    if div is not None:
+        assert first_tie is not None and div >= first_tie, (
+            f"free-running token {div} differs (gpu {toks_g[div]} oracle {toks_o[div]}) before the "
+            f"first near tie {first_tie}")
+
+
+@pytest.mark.timeout(400)
+def test_decode_28_layers_fp16_greedy_parity(mdx, gpu, oracle_lib, full):
     cfg, get = full
     path = get(0, 1003)
     max_seq = 512 + 64 + 8
     g = mdx.Decoder(path, cfg, "fp16", max_seq)
     o = oracle_lib.Model(path, FULL, 0, max_seq, kv_fp16=True)
-    g.kv_fill_normal(512, 1003)
-    assert o.kv_fill_normal(512, 1003) == 0
-    tg, lg = g.step(START)
-    to, lo = o.step(START)
-    print(f"step0: gpu {tg} oracle {to} cos {cosine(lg, lo):.7f} rel {rel_err(lg, lo):.2e}")
-    # logits after 28 layers: the bar is cosine (the 1e-3 bound is per projection,
-    # checked kernel by kernel in test_gpu_kernels.py)
-    assert cosine(lg, lo) >= 0.9999 and tg == to
-    toks_g, _ = g.generate_greedy(tg, 63)
-    toks_o, margins = o.greedy(to, 63)
-    i = _first_divergence(toks_g, toks_o)
-    print(f"min top1-top2 margin {min(margins):.4g}; first divergence {i}")
-    assert i is None, f"token {i + 1}: gpu {toks_g[i]} oracle {toks_o[i]} margin {margins[i]:.3g}"
+    _greedy_parity(mdx, oracle_lib, g, o, path, 0, max_seq, 512, 1003, 64)
 
 
 def test_prefill_m60_int8_then_lm_head_matches_oracle(mdx, gpu, oracle_lib, full):
@@ -92,20 +154,11 @@ def test_prefill_m60_int8_then_lm_head_matches_oracle(mdx, gpu, oracle_lib, full
     assert tg == to and cosine(lg2, lo2) >= 0.9999
 
 
-@pytest.mark.timeout(400)
+@pytest.mark.timeout(600)
 def test_w4a16_long_context_128_steps(mdx, gpu, oracle_lib, full):
     cfg, get = full
     path = get(2, 1005)
     max_seq = 4224
     g = mdx.Decoder(path, cfg, "int4", max_seq)
     o = oracle_lib.Model(path, FULL, 2, max_seq, kv_fp16=True)
-    g.kv_fill_normal(4096, 1005)
-    assert o.kv_fill_normal(4096, 1005) == 0
-    tg, lg = g.step(START)
-    to, lo = o.step(START)
-    assert cosine(lg, lo) >= 0.9999 and tg == to
-    toks_g, _ = g.generate_greedy(tg, 127)
-    toks_o, margins = o.greedy(to, 127)
-    i = _first_divergence(toks_g, toks_o)
-    print(f"min top1-top2 margin {min(margins):.4g}; first divergence {i}")
-    assert i is None, f"token {i + 1}: gpu {toks_g[i]} oracle {toks_o[i]} margin {margins[i]:.3g}"
+    _greedy_parity(mdx, oracle_lib, g, o, path, 2, max_seq, 4096, 1005, 128)

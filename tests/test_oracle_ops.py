@@ -238,6 +238,32 @@ def test_matmul_f16_float64(oracle_lib):
     assert np.array_equal(yi, (xi.astype(np.int64) @ wi.astype(np.int64)).astype(np.float32))
 
 
+def test_matmul_accumulation_orders(oracle_lib):
+    """Order 1 (four interleaved sums) is a second valid accumulation order:
+    exact on integer-valued operands like order 0, within fp32 rounding of
+    the float64 product on general data, different from order 0 in the last
+    bits, and order 0 is what the oracle uses unless switched."""
+    rng = np.random.default_rng(11)
+    M, K, N = 2, 1024, 256
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) * 0.02).astype(np.float16)
+    q = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    want = x.astype(np.float16).astype(np.float64) @ w.astype(np.float64)
+    xi = rng.integers(-16, 17, (M, K)).astype(np.float32)
+    exact = (xi.astype(np.int64) @ q.astype(np.int64)).astype(np.float32)
+    ys = {}
+    try:
+        for order in (0, 1):
+            oracle_lib.lib().orc_set_accum_order(order)
+            ys[order] = oracle_lib.matmul(0, x, w.view(np.uint16), None, M, K, N)
+            assert rel_err(ys[order], want) < 1e-5
+            assert np.array_equal(oracle_lib.matmul(1, xi, q, None, M, K, N), exact)
+    finally:
+        oracle_lib.lib().orc_set_accum_order(0)
+    assert not np.array_equal(ys[0], ys[1])
+    assert np.array_equal(oracle_lib.matmul(0, x, w.view(np.uint16), None, M, K, N), ys[0])
+
+
 @pytest.mark.parametrize("K,N", [(1024, 4096), (3072, 64), (48, 1000)])
 def test_matmul_i8_known_answer_bit_exact(oracle_lib, K, N):
     rng = np.random.default_rng(K + N)
