@@ -115,7 +115,12 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter runs: a 256 MiB device copy (the calibration kernel), then the "
+                         "decode steps only")
     args = ap.parse_args()
+    if args.probe:
+        args.no_prefill = args.no_cpu_baseline = True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the decoder on a single MI355X and has "
               "no multi-GPU path (see DESIGN.md for how it would shard); use --gpus 1.",
@@ -132,6 +137,13 @@ def main() -> int:
              tie_word_embeddings=1, has_qk_norm=1, rope_style=1, max_batch_prefill=64)
     cfg = mdx.qwen3_0_6b_config(name="qwen3-0.6b-synthetic", **d)
     max_seq = KV_PREFILL + max(args.steps, args.warmup) + 8
+
+    if args.probe:
+        # plain copy of a known size: the scale for the HBM byte counters
+        if mdx.lib().mdx_copy_probe(1 << 28, 3) != 0:
+            print("bench.py: copy probe failed", file=sys.stderr)
+            return 1
+        log("probe copy: 3 x 256 MiB device-to-device")
 
     # ---- decode (config: 28-layer greedy, FP16 layers + INT8 lm_head, KV 512) ----
     path16 = model_dir(mdx, "decode_fp16_seed1003", cfg, 0, 1003)
@@ -150,17 +162,20 @@ def main() -> int:
     log(f"decode: {ms_per_step * 1000:.1f} us/token wall, {dev_ms * 1000 / args.steps:.1f} us/token device")
 
     # API-level latency: matmul_decoder_step with logits copied to the host each token
-    dec.kv_fill_normal(KV_PREFILL, 1003)
-    logits = np.empty(d["vocab_size"], np.float32)
-    tok, t0 = START_TOKEN, time.perf_counter()
-    n_api = min(args.steps, 32)
-    for _ in range(n_api):
-        tok, _ = dec.step(tok)
-    api_ms = (time.perf_counter() - t0) * 1000.0 / n_api
+    api_ms = None
+    if not args.probe:
+        dec.kv_fill_normal(KV_PREFILL, 1003)
+        tok, t0 = START_TOKEN, time.perf_counter()
+        n_api = min(args.steps, 32)
+        for _ in range(n_api):
+            tok, _ = dec.step(tok)
+        api_ms = round((time.perf_counter() - t0) * 1000.0 / n_api, 4)
 
-    # per-projection kernels (each launch cycles through the 28 layers' weights)
+    # per-projection kernels of the per-stage path (each launch cycles through
+    # the 28 layers' weights)
     kernels = {}
-    for name, per_step in (("qkv", 28), ("o", 28), ("gate_up", 28), ("down", 28), ("lm_head", 1)):
+    for name, per_step in () if args.probe else (("qkv", 28), ("o", 28), ("gate_up", 28),
+                                                 ("down", 28), ("lm_head", 1)):
         iters = 280 if per_step == 28 else 40
         dec.time_projection(name, 28)
         us, b = dec.time_projection(name, iters)
@@ -225,7 +240,7 @@ def main() -> int:
                      "traffic": traffic,
                      "bytes_per_launch": bytes_step, "avg_us": round(step_us, 2)},
         "wall_roofline_frac": round(bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "api_step_ms": round(api_ms, 4),
+        "api_step_ms": api_ms,
         "per_stage_path_kernels": kernels,
         "prefill_m60": prefill,
         "cpu_baseline": cpu,

@@ -31,6 +31,9 @@ const char* mdx_version(void);
 int mdx_device_count(void);
 /* Last HIP runtime message recorded by the library (thread-local). */
 const char* mdx_last_error(void);
+/* `iters` device-to-device copies of `bytes` (a plain copy kernel of known
+ * traffic: the calibration run for HBM byte counters). */
+int mdx_copy_probe(size_t bytes, int iters);
 
 /* Decode path of a context: 1 when a step is one cooperative launch of the
  * whole model (the 0.6B shape with one weight kind and the INT8 lm_head;

@@ -1298,6 +1298,19 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
 const char* mdx_version(void) { return "1.0.0 gfx950"; }
 int mdx_device_count(void) { return mdxrt_device_count(); }
 
+int mdx_copy_probe(size_t bytes, int iters) {
+    if (bytes == 0 || iters <= 0) return MATMUL_DECODER_ERR_INVALID_ARG;
+    void *a = NULL, *b = NULL, *s = NULL;
+    int rc = mdxrt_malloc(&a, bytes) || mdxrt_malloc(&b, bytes) || mdxrt_stream_create(&s);
+    if (!rc) rc = mdxrt_fill_u32(a, 0x3f800000u, bytes / 4, s);
+    for (int i = 0; i < iters && !rc; i++) rc = mdxrt_d2d_async(b, a, bytes, s);
+    if (!rc) rc = mdxrt_stream_sync(s);
+    if (s) mdxrt_stream_destroy(s);
+    mdxrt_free(a);
+    mdxrt_free(b);
+    return rc ? MATMUL_DECODER_ERR_RKNN : 0;
+}
+
 int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* out, int cap) {
     if (!c || !out) return MATMUL_DECODER_ERR_INVALID_ARG;
     if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;

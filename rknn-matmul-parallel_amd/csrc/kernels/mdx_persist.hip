@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 
 #include "mdx_common.h"
 #include "mdx_device.h"
@@ -1026,6 +1027,18 @@ int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
     a.trace = p->trace;
     a.trace_stride = p->trace_stride;
     if (a.trace && a.trace_stride < 16 * a.n_layers + 4) return -1;
+    // MDX_COOP=0 issues the same grid as an ordinary launch (for tools that do
+    // not follow cooperative launches).  The grid still fits the device one
+    // workgroup per CU, and every wait is bounded, so a workgroup that did
+    // not become resident would end the step with an error, not a hang.
+    static const int coop = [] {
+        const char* e = getenv("MDX_COOP");
+        return !(e && e[0] == '0');
+    }();
+    if (!coop) {
+        hipLaunchKernelGGL(k, dim3(NB), dim3(NT), 0, (hipStream_t)stream, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     void* args[] = {&a};
     hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(k), dim3(NB), dim3(NT),
                                               args, 0, (hipStream_t)stream);

@@ -105,6 +105,7 @@ def lib() -> C.CDLL:
             "rmp_get_single_core_time": (C.c_float, [P]),
             "mdx_version": (C.c_char_p, []),
             "mdx_device_count": (C.c_int, []),
+            "mdx_copy_probe": (C.c_int, [C.c_size_t, C.c_int]),
             "mdx_last_error": (C.c_char_p, []),
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
             "mdx_decode_path": (C.c_int, [P]),
