@@ -113,6 +113,7 @@ int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* sc
     float* dy = rc ? NULL : (float*)dalloc(&s, (size_t)M * N * 4);
     float* scr = rc ? NULL : (float*)dalloc(&s, mdx_gemm_scratch_floats(M, N, K) * 4);
     if (!rc && (!dx || !dx16 || !dy || !scr)) rc = MATMUL_DECODER_ERR_MEMORY;
+    if (!rc) rc = mdxrt_fill_u32(scr, 0u, mdx_gemm_scratch_floats(M, N, K), s.stream);
     if (!rc) rc = mdxrt_h2d(dx, x, (size_t)M * K * 4);
     if (!rc) rc = mdx_launch_to_f16(dx, M * K, dx16, s.stream);
     if (!rc) rc = mdx_launch_gemm(dx16, M, &d, 0, dy, scr, s.stream);

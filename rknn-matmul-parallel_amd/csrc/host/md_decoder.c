@@ -527,11 +527,13 @@ static int run_head(MatmulDecoderContext* c, const mdx_wdesc* lm, int* out_token
 
 static int run_prefill(MatmulDecoderContext* c, int M, void* s) {
     const float eps = c->config.rms_eps;
-    int rc = 0;
+    /* the first layer's input norm; every later norm is fused into the
+     * residual projection before it */
+    int rc = mdx_launch_rmsnorm_rows(c->d_bhidden, c->layers[0].in_norm, eps, M, c->d, c->d_bx16, s);
     for (int l = 0; l < c->L && rc == 0; l++) {
         md_layer* ly = &c->layers[l];
-        rc = mdx_launch_rmsnorm_rows(c->d_bhidden, ly->in_norm, eps, M, c->d, c->d_bx16, s);
-        if (!rc) rc = mdx_launch_gemm(c->d_bx16, M, &ly->qkv, 0, c->d_bqkv, c->d_gscr, s);
+        const float* next_norm = l + 1 < c->L ? c->layers[l + 1].in_norm : NULL;
+        rc = mdx_launch_gemm(c->d_bx16, M, &ly->qkv, 0, c->d_bqkv, c->d_gscr, s);
         if (!rc)
             rc = mdx_launch_qk_rope_append_rows(c->d_state, c->d_bqkv, M, ly->q_norm, ly->k_norm,
                                                 eps, c->d_cos, c->d_sin, c->nq, c->nkv, c->hd,
@@ -539,10 +541,13 @@ static int run_prefill(MatmulDecoderContext* c, int M, void* s) {
         if (!rc)
             rc = mdx_launch_attn_prefill(c->d_state, c->d_bq, M, ly->kc, ly->vc, c->nq, c->nkv,
                                          c->hd, c->d_battn16, s);
-        if (!rc) rc = mdx_launch_gemm(c->d_battn16, M, &ly->o, 1, c->d_bhidden, c->d_gscr, s);
-        if (!rc) rc = mdx_launch_rmsnorm_rows(c->d_bhidden, ly->post_norm, eps, M, c->d, c->d_bx16, s);
+        if (!rc)
+            rc = mdx_launch_gemm_residual_norm(c->d_battn16, M, &ly->o, c->d_bhidden, ly->post_norm,
+                                               eps, c->d_bx16, c->d_gscr, s);
         if (!rc) rc = mdx_launch_gemm(c->d_bx16, M, &ly->gu, 2, c->d_bact16, c->d_gscr, s);
-        if (!rc) rc = mdx_launch_gemm(c->d_bact16, M, &ly->down, 1, c->d_bhidden, c->d_gscr, s);
+        if (!rc)
+            rc = mdx_launch_gemm_residual_norm(c->d_bact16, M, &ly->down, c->d_bhidden, next_norm,
+                                               eps, c->d_bx16, c->d_gscr, s);
     }
     if (!rc) rc = mdx_launch_advance(c->d_state, M, s);
     return rc;

@@ -61,6 +61,8 @@ RmpContext* rmp_create(const RmpConfig* config, const void* weights, const float
     if (!rc) rc = mdxrt_malloc((void**)&c->d_x, (size_t)M * K * 2);
     if (!rc) rc = mdxrt_malloc((void**)&c->d_y, (size_t)M * N * 4);
     if (!rc) rc = mdxrt_malloc((void**)&c->d_scratch, mdx_gemm_scratch_floats(mchunk, N, K) * 4);
+    if (!rc) rc = mdxrt_fill_u32(c->d_scratch, 0u, mdx_gemm_scratch_floats(mchunk, N, K), c->stream);
+    if (!rc) rc = mdxrt_stream_sync(c->stream);
     if (!rc) rc = mdxrt_h2d(c->d_w, rows, (size_t)K * N * 2);
     free(rows);
     if (rc) {

@@ -190,10 +190,17 @@ int mdx_launch_to_f16(const float* x, int n, uint16_t* x16, void* stream);
 
 /* Y = X16[M][K] . W^T on MFMA, M <= 64.  epilogue: 0 store fp32 y[M][N],
  * 1 add into y[M][N], 2 SwiGLU (rows [0,N/2) gate, [N/2,N) up) -> fp16
- * act[M][N/2].  scratch: mdx_gemm_scratch_floats(M, N, K) floats. */
-size_t mdx_gemm_scratch_floats(int M, int N, int K);
+ * act[M][N/2].  `scratch` is not used (kept for the signature). */
 int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
                     float* scratch, void* stream);
+/* Residual projection with the next RMSNorm fused: hidden[M][N] += X16 . W^T
+ * (x scale), then x16_out[M][N] = fp16((hidden * rms) * norm_w) per row
+ * (norm_w NULL: no norm).  K is split over blocks; scratch holds the split
+ * partials: mdx_gemm_scratch_floats(M, N, K) floats. */
+size_t mdx_gemm_scratch_floats(int M, int N, int K);
+int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w, float* hidden,
+                                  const float* norm_w, float eps, uint16_t* x16_out, float* scratch,
+                                  void* stream);
 
 /* QK-norm + RoPE for rows t < M at positions start+t, appending k,v fp16
  * at cache rows start+t; q written fp32 [M][nq*hd].  `start` is read from

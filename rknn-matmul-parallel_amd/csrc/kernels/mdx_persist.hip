@@ -318,27 +318,6 @@ __device__ __forceinline__ void cm_dot(const uint4 (&w)[NWT], const uint4* xs4, 
 
 // ---- small helpers ----------------------------------------------------------
 
-// Cross-lane reductions with DPP moves (a few cycles each, unlike LDS-routed
-// shuffles).  row_sum16: every lane of each 16-lane row gets the row's sum.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-__device__ __forceinline__ float row_sum16(float v) {
-    v = v + dpp<0xB1>(v);    // quad_perm [1,0,3,2]
-    v = v + dpp<0x4E>(v);    // quad_perm [2,3,0,1]
-    v = v + dpp<0x124>(v);   // row_ror:4
-    v = v + dpp<0x128>(v);   // row_ror:8
-    return v;
-}
-// Sum over the 64 lanes, returned to every lane (through lane 63).
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v = row_sum16(v);
-    v = v + dpp<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
-    v = v + dpp<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
 __device__ __forceinline__ float block_sum4(float v, float* ws, int t) {
     v = wave_sum_dpp(v);
     if ((t & 63) == 0) ws[t >> 6] = v;

@@ -1,13 +1,8 @@
 // mdx_prefill.hip — batch prefill (M <= 64 rows) kernels for gfx950.
 //
 // Projections (reference: src/matmul_decoder.c:1841-1899, run_batch_matmul)
-// run on MFMA v_mfma_f32_16x16x32_f16: a block owns a 64 x 32 output tile
-// (all M rows, 32 weight rows of W^T) over a K range; int8/int4 weights are
-// widened to fp16 exactly while being staged into LDS, and the next K chunk
-// is fetched into registers while the current one is multiplied.  Split-K
-// partials are summed in a second pass that applies the per-column scale and
-// the epilogue (residual add or SwiGLU), so the result does not depend on
-// scheduling.
+// run on MFMA v_mfma_f32_16x16x32_f16, one block per 64 x 32 output tile with
+// the K range split over its waves (see k_gemm).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -21,8 +16,6 @@ namespace {
 
 constexpr int kMaxM = 64;
 constexpr int kNT = 32;        // weight rows (output columns) per block
-constexpr int kKC = 128;       // K per staged chunk
-constexpr int kLdsStride = kKC + 8;   // halfs per LDS row (pad against bank conflicts)
 
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* x, const float* w, float eps,
                                                        int d, uint16_t* x16) {
@@ -44,17 +37,44 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
         x16[i] = f32_to_f16_bits(x[i]);
 }
 
-// Bytes of one staged chunk row (kKC elements) for each weight kind.
-template <int KIND> struct Stage;
-template <> struct Stage<MDX_W_F16> { static constexpr int RB = kKC * 2; };
-template <> struct Stage<MDX_W_I8> { static constexpr int RB = kKC; };
-template <> struct Stage<MDX_W_I4> { static constexpr int RB = kKC / 2; };
-// 16-byte pieces per chunk = kNT * RB / 16; pieces per thread = that / 256.
+// ---- projections: register-direct MFMA GEMM ----------------------------------
+//
+// Block = 4 waves (one per SIMD, so each may hold 512 registers), one 64 x 32 output tile (all M rows, two 16-column MFMA
+// tiles; for SwiGLU the gate and up columns of the same 16 features).  The K
+// range is split over the waves in contiguous runs of K-blocks; a wave keeps
+// two rounds of K-blocks of weights and activations in flight in registers (the MFMA
+// fragments are loaded straight from memory, the int8/int4 weights widened to
+// fp16 exactly in registers), so a block's loads are not serialised behind
+// barriers.  The 4 partial tiles are summed in LDS in wave order, then the
+// scale and the epilogue are applied.
+//
+// K-block layout: a weight load is 16 bytes per lane = EPL consecutive k of
+// one weight row (EPL = 8 fp16, 16 int8, 32 int4), lane group g = lane/16
+// takes k [g*EPL, (g+1)*EPL) of the block, and MFMA step s of the block uses
+// k g*EPL + 8s .. +7; the activations are loaded with the same k mapping.
 
+template <int KIND> struct GemmKind;
+// NKB K-blocks per round; two rounds are in flight (the next one is requested
+// before the current one is multiplied).
+template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 8; };
+template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 4; };
+template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 2; };
+
+constexpr int kGemmWaves = 4;
+
+// Weight row of tile column c: 32 consecutive rows, or for SwiGLU the 16 gate
+// rows f0.. and the 16 up rows N/2+f0.. of the same features.
+__device__ __forceinline__ int tile_row(int tile, int c, int swiglu, int N) {
+    if (!swiglu) return tile * kNT + c;
+    const int f0 = tile * (kNT / 2);
+    return c < kNT / 2 ? f0 + c : N / 2 + f0 + (c - kNT / 2);
+}
+
+// 16 weight bytes -> the EPL/8 fp16 B fragments of this lane.
 template <int KIND>
-__device__ __forceinline__ void widen_store(uint4 v, uint16_t* dst /* LDS, 8/16/32 halfs */) {
+__device__ __forceinline__ void widen_b(uint4 v, half8_t* out) {
     if constexpr (KIND == MDX_W_F16) {
-        *reinterpret_cast<uint4*>(dst) = v;
+        out[0] = __builtin_bit_cast(half8_t, v);
     } else if constexpr (KIND == MDX_W_I8) {
         const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
         uint32_t o[8];
@@ -65,8 +85,8 @@ __device__ __forceinline__ void widen_store(uint4 v, uint16_t* dst /* LDS, 8/16/
             o[2 * i] = h2_bits(a);
             o[2 * i + 1] = h2_bits(b);
         }
-        *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<uint4*>(dst + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+        out[0] = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+        out[1] = __builtin_bit_cast(half8_t, make_uint4(o[4], o[5], o[6], o[7]));
     } else {
         const uint32_t wd[4] = {v.x ^ 0x88888888u, v.y ^ 0x88888888u, v.z ^ 0x88888888u,
                                 v.w ^ 0x88888888u};
@@ -74,137 +94,209 @@ __device__ __forceinline__ void widen_store(uint4 v, uint16_t* dst /* LDS, 8/16/
         for (int i = 0; i < 4; i++) {
             uint32_t o[4];
 #pragma unroll
-            for (int p = 0; p < 4; p++) o[p] = h2_bits(i4_pair(wd[i], p));
-            *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+            for (int q = 0; q < 4; q++) o[q] = h2_bits(i4_pair(wd[i], q));
+            out[i] = __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
         }
     }
 }
 
-// grid = (ceil(N / 32), nsplit); block 256 = 4 waves, wave w owns rows
-// [16w, 16w+16) of the M dimension and both 16-column MFMA tiles.
 template <int KIND>
-__global__ __launch_bounds__(256) void k_gemm(const uint16_t* x16, int M, const uint8_t* w, int K,
-                                              int N, int kchunks_per_split, float* part) {
-    constexpr int RB = Stage<KIND>::RB;
-    constexpr int EPP = 16 * kKC / RB;                       // elements per 16-byte piece
-    constexpr int PIECES = kNT * RB / 16;
-    constexpr int PPT = PIECES / 256 > 0 ? PIECES / 256 : 1; // pieces per thread
-    __shared__ __attribute__((aligned(16))) uint16_t bs[kNT * kLdsStride];
+struct GemmRound {
+    uint4 bw[GemmKind<KIND>::NKB][2];
+    uint4 av[GemmKind<KIND>::NKB][4][GemmKind<KIND>::EPL / 8];
+};
+
+// Requests the NKB K-blocks of a round starting at K-block kb (blocks past
+// the wave's range re-read block kb_last; gemm_compute skips them).
+template <int KIND>
+__device__ __forceinline__ void gemm_issue(GemmRound<KIND>& R, int kb, int kb_last,
+                                           const uint8_t* const (&wrow)[2], const bool (&wvalid)[2],
+                                           const uint16_t* const (&arow)[4], int g) {
+    using GK = GemmKind<KIND>;
+    constexpr int EPL = GK::EPL, KB = 4 * EPL;
+#pragma unroll
+    for (int j = 0; j < GK::NKB; j++) {
+        const int k = min(kb + j, kb_last) * KB + g * EPL;
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+            R.bw[j][t] = wvalid[t] ? *reinterpret_cast<const uint4*>(wrow[t] + (size_t)k * 16 / EPL)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int s = 0; s < EPL / 8; s++)
+                R.av[j][r][s] = *reinterpret_cast<const uint4*>(arow[r] + k + 8 * s);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void gemm_compute(const GemmRound<KIND>& R, int kb, int kb_end,
+                                             float4_t (&acc)[2][4]) {
+    using GK = GemmKind<KIND>;
+    constexpr int STEPS = GK::EPL / 8;
+#pragma unroll
+    for (int j = 0; j < GK::NKB; j++) {
+        if (kb + j >= kb_end) break;
+        half8_t b[2][STEPS];
+#pragma unroll
+        for (int t = 0; t < 2; t++) widen_b<KIND>(R.bw[j][t], b[t]);
+#pragma unroll
+        for (int s = 0; s < STEPS; s++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const half8_t a = __builtin_bit_cast(half8_t, R.av[j][r][s]);
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+                    acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[t][s], acc[t][r], 0, 0, 0);
+            }
+    }
+}
+
+// With part != NULL each block covers K split blockIdx.y (of gridDim.y,
+// possibly 1) and stores its raw partial tile to part[blockIdx.y][row][N]
+// for k_residual_norm; with part == NULL gridDim.y is 1 and the epilogue
+// writes out_f32 / out_f16.
+template <int KIND>
+__global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, int M,
+                                                          const uint8_t* w, int K, int N,
+                                                          const float* scale, int epi,
+                                                          float* out_f32, uint16_t* out_f16,
+                                                          float* part) {
+    using GK = GemmKind<KIND>;
+    constexpr int EPL = GK::EPL, KB = 4 * EPL;
+    __shared__ float red[kGemmWaves][kMaxM * kNT];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n0 = blockIdx.x * kNT;
-    const int nkc = (K + kKC - 1) / kKC;
-    const int c_begin = blockIdx.y * kchunks_per_split;
-    const int c_end = min(nkc, c_begin + kchunks_per_split);
-    const size_t row_bytes = (size_t)K * (KIND == MDX_W_F16 ? 2 : 1) / (KIND == MDX_W_I4 ? 2 : 1);
+    const int tile = blockIdx.x;
+    const int swiglu = epi == 2;
+    const int g = lane >> 4, c16 = lane & 15;
+    const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
+    // this block's K-blocks (split blockIdx.y of gridDim.y), then this wave's: [kb0, kb1)
+    const int nkb_all = K / KB;
+    const int per_split = (nkb_all + gridDim.y - 1) / gridDim.y;
+    const int sb0 = min(nkb_all, (int)blockIdx.y * per_split);
+    const int sb1 = min(nkb_all, sb0 + per_split);
+    const int per = (sb1 - sb0 + kGemmWaves - 1) / kGemmWaves;
+    const int kb0 = min(sb1, sb0 + wave * per), kb1 = min(sb1, kb0 + per);
 
-    float4_t acc[2];
-    acc[0] = float4_t{0.f, 0.f, 0.f, 0.f};
-    acc[1] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const uint8_t* wrow_[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) wrow_[t] = w + (size_t)tile_row(tile, 16 * t + c16, swiglu, N) * row_bytes;
+    const uint8_t* const wrow[2] = {wrow_[0], wrow_[1]};
+    const bool wvalid[2] = {tile_row(tile, c16, swiglu, N) < N, tile_row(tile, 16 + c16, swiglu, N) < N};
+    const uint16_t* const arow[4] = {x16 + (size_t)min(c16, M - 1) * K, x16 + (size_t)min(16 + c16, M - 1) * K,
+                                     x16 + (size_t)min(32 + c16, M - 1) * K, x16 + (size_t)min(48 + c16, M - 1) * K};
 
-    const int arow = 16 * wave + (lane & 15);
-    const int kq = 8 * (lane >> 4);            // this lane's k offset inside a 32-wide step
+    float4_t acc[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto load_chunk = [&](int c, uint4* regs) {
-#pragma unroll
-        for (int p = 0; p < PPT; p++) {
-            const int piece = tid + p * 256;
-            regs[p] = make_uint4(0, 0, 0, 0);
-            if (piece < PIECES) {
-                const int r = piece / (RB / 16), q = piece % (RB / 16);
-                const int n = n0 + r;
-                const size_t off = (size_t)c * RB + (size_t)q * 16;
-                if (n < N && off + 16 <= row_bytes)
-                    regs[p] = *reinterpret_cast<const uint4*>(w + (size_t)n * row_bytes + off);
-            }
-        }
-    };
-    auto store_chunk = [&](const uint4* regs) {
-#pragma unroll
-        for (int p = 0; p < PPT; p++) {
-            const int piece = tid + p * 256;
-            if (piece < PIECES) {
-                const int r = piece / (RB / 16), q = piece % (RB / 16);
-                widen_store<KIND>(regs[p], bs + r * kLdsStride + q * EPP);
-            }
-        }
-    };
-
-    uint4 regs[PPT];
-    if (c_begin < c_end) load_chunk(c_begin, regs);
-    for (int c = c_begin; c < c_end; c++) {
-        __syncthreads();
-        store_chunk(regs);
-        __syncthreads();
-        if (c + 1 < c_end) load_chunk(c + 1, regs);
-        const int kbase = c * kKC;
-#pragma unroll
-        for (int ks = 0; ks < kKC; ks += 32) {
-            const int k = kbase + ks + kq;
-            half8_t a = {};
-            if (arow < M && k + 8 <= K)
-                a = *reinterpret_cast<const half8_t*>(x16 + (size_t)arow * K + k);
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const half8_t b =
-                    *reinterpret_cast<const half8_t*>(bs + (16 * t + (lane & 15)) * kLdsStride + ks + kq);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
-            }
+    if (kb0 < kb1) {
+        GemmRound<KIND> ra, rb;
+        gemm_issue<KIND>(ra, kb0, kb1 - 1, wrow, wvalid, arow, g);
+        for (int kb = kb0; kb < kb1; kb += 2 * GK::NKB) {
+            const int kb_b = kb + GK::NKB, kb_a2 = kb + 2 * GK::NKB;
+            if (kb_b < kb1) gemm_issue<KIND>(rb, kb_b, kb1 - 1, wrow, wvalid, arow, g);
+            gemm_compute<KIND>(ra, kb, kb1, acc);
+            if (kb_a2 < kb1) gemm_issue<KIND>(ra, kb_a2, kb1 - 1, wrow, wvalid, arow, g);
+            if (kb_b < kb1) gemm_compute<KIND>(rb, kb_b, kb1, acc);
         }
     }
 
-    float* out = part + (size_t)blockIdx.y * kMaxM * N;
+    // D fragment: lane holds column c16 of MFMA tile t, rows 16r + 4g + i
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int col = n0 + 16 * t + (lane & 15);
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = 16 * wave + 4 * (lane >> 4) + i;
-            if (row < M && col < N) out[(size_t)row * N + col] = acc[t][i];
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                red[wave][(16 * r + 4 * g + i) * kNT + 16 * t + c16] = acc[t][r][i];
+    __syncthreads();
+    // 2048 outputs over 256 threads, summed in wave order
+    for (int o = tid; o < kMaxM * kNT; o += kGemmWaves * 64) {
+        const int row = o / kNT, col = o % kNT;
+        if (row >= M) continue;
+        float v = red[0][o];
+#pragma unroll
+        for (int wv = 1; wv < kGemmWaves; wv++) v = v + red[wv][o];
+        if (part) {
+            const int n = tile * kNT + col;
+            if (n < N) part[((size_t)blockIdx.y * kMaxM + row) * N + n] = v;
+            continue;
         }
-    }
-}
-
-// Sums split partials, applies scale and the epilogue.  grid over outputs.
-__global__ void k_gemm_reduce(const float* part, int nsplit, int M, int N, const float* scale,
-                              int epi, float* out_f32, uint16_t* out_f16) {
-    const int cols = epi == 2 ? N / 2 : N;
-    const int total = M * cols;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-        const int m = i / cols, n = i % cols;
-        if (epi == 2) {
-            float g = 0.0f, u = 0.0f;
-            for (int s = 0; s < nsplit; s++) {
-                g += part[((size_t)s * kMaxM + m) * N + n];
-                u += part[((size_t)s * kMaxM + m) * N + n + cols];
-            }
-            if (scale) {
-                g = g * scale[n];
-                u = u * scale[n + cols];
-            }
-            float v;
-            if (n < (cols & ~3)) v = silu_mul(g, u);
-            else v = (g / (1.0f + expf(-g))) * u;
-            out_f16[(size_t)m * cols + n] = f32_to_f16_bits(v);
+        if (swiglu) {
+            if (col >= kNT / 2) continue;
+            const int cols = N / 2;
+            const int f = tile * (kNT / 2) + col;
+            if (f >= cols) continue;
+            float u = red[0][row * kNT + col + kNT / 2];
+#pragma unroll
+            for (int wv = 1; wv < kGemmWaves; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
+            const float gs = v * (scale ? scale[f] : 1.0f), us = u * (scale ? scale[cols + f] : 1.0f);
+            float act;
+            if (f < (cols & ~3)) act = silu_mul(gs, us);
+            else act = (gs / (1.0f + expf(-gs))) * us;     // reference tail formula
+            out_f16[(size_t)row * cols + f] = f32_to_f16_bits(act);
         } else {
-            float y = 0.0f;
-            for (int s = 0; s < nsplit; s++) y += part[((size_t)s * kMaxM + m) * N + n];
-            if (scale) y = y * scale[n];
-            if (epi == 1) out_f32[(size_t)m * N + n] = out_f32[(size_t)m * N + n] + y;
-            else out_f32[(size_t)m * N + n] = y;
+            const int n = tile * kNT + col;
+            if (n >= N) continue;
+            const float y = v * (scale ? scale[n] : 1.0f);
+            if (epi == 1) out_f32[(size_t)row * N + n] = out_f32[(size_t)row * N + n] + y;
+            else out_f32[(size_t)row * N + n] = y;
         }
     }
 }
 
-int plan_splits(int N, int K, int* chunks_per_split) {
-    const int ntiles = (N + kNT - 1) / kNT;
-    const int nkc = (K + kKC - 1) / kKC;
-    int ns = (384 + ntiles - 1) / ntiles;
-    if (ns > nkc) ns = nkc;
-    if (ns < 1) ns = 1;
-    const int cps = (nkc + ns - 1) / ns;
-    *chunks_per_split = cps;
-    return (nkc + cps - 1) / cps;
+// Split-K finish for the o and down projections: y = sum of the split
+// partials (split order) x scale; hidden += y (the residual); then the next
+// RMSNorm of the row, x16 = fp16((hidden * rms) * norm_w) (skipped when norm_w
+// is NULL).  grid = M rows, 256 threads.
+constexpr int kMaxSplits = 16;
+
+__global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns, int N,
+                                                       const float* scale, float* hidden,
+                                                       const float* norm_w, float eps,
+                                                       uint16_t* x16) {
+    __shared__ float ws[4];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    float* hr = hidden + (size_t)m * N;
+    float ss = 0.0f;
+    // thread t owns columns 4t..4t+3 (+1024 per round); every load of a round
+    // is issued before any of them is used
+    for (int c = 4 * tid; c < N; c += 1024) {
+        float4 p[kMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplits; sp++)
+            if (sp < ns) p[sp] = *reinterpret_cast<const float4*>(part + ((size_t)sp * kMaxM + m) * N + c);
+        const float4 h0 = *reinterpret_cast<const float4*>(hr + c);
+        const float4 sc = scale ? *reinterpret_cast<const float4*>(scale + c) : make_float4(1.f, 1.f, 1.f, 1.f);
+        float4 y = p[0];
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplits; sp++)
+            if (sp < ns) {
+                y.x = y.x + p[sp].x; y.y = y.y + p[sp].y; y.z = y.z + p[sp].z; y.w = y.w + p[sp].w;
+            }
+        float4 h;
+        h.x = h0.x + y.x * sc.x; h.y = h0.y + y.y * sc.y; h.z = h0.z + y.z * sc.z; h.w = h0.w + y.w * sc.w;
+        *reinterpret_cast<float4*>(hr + c) = h;
+        ss += h.x * h.x + h.y * h.y + h.z * h.z + h.w * h.w;
+    }
+    if (!norm_w) return;
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) ws[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = ws[0] + ws[1] + ws[2] + ws[3];
+    const float rms = 1.0f / sqrtf(tot / (float)N + eps);
+    for (int c = 4 * tid; c < N; c += 1024) {
+        const float4 h = *reinterpret_cast<const float4*>(hr + c);
+        const float4 w = *reinterpret_cast<const float4*>(norm_w + c);
+        uint2 o;
+        o.x = (uint32_t)f32_to_f16_bits((h.x * rms) * w.x) | ((uint32_t)f32_to_f16_bits((h.y * rms) * w.y) << 16);
+        o.y = (uint32_t)f32_to_f16_bits((h.z * rms) * w.z) | ((uint32_t)f32_to_f16_bits((h.w * rms) * w.w) << 16);
+        *reinterpret_cast<uint2*>(x16 + (size_t)m * N + c) = o;
+    }
 }
 
 // QK-norm + RoPE + append for M rows (reference: src/matmul_decoder.c:1984-2034,
@@ -262,111 +354,147 @@ __global__ __launch_bounds__(64) void k_qk_rope_append_rows(
 
 // Causal attention for one query row and one KV head group (reference:
 // src/cpu_ops.c:459-571, over the cache rows that already hold the batch's
-// own K/V).  grid = (nkv, M), 256 threads; positions are streamed in tiles
-// of 16 with a running max and sum.
+// own K/V).  grid = (nkv, M), 256 threads.  Positions [0, pos+t] go in rounds
+// of PP passes; a pass gives each position HD/8 lanes (8 dimensions each).
+// Every K/V row of a round is requested before any is used; scores of all
+// passes, one workgroup-wide max per head, P.V summed over the position
+// groups in LDS, and the rounds merged with the usual rescaling.
+template <int LP>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (LP == 16) return row_sum16(v);
+    else return group_sum(v, LP);
+}
+
 template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn_prefill(const mdx_state* st, const float* q,
                                                       const uint16_t* kc, const uint16_t* vc,
                                                       int nkv, uint16_t* out16) {
-    constexpr int LP = HD / 8;
-    constexpr int PPW = 64 / LP;
-    constexpr int TILE = 4 * PPW;       // positions scored per tile
-    constexpr int PG = 256 / LP;
+    constexpr int LP = HD / 8;          // lanes per position
+    constexpr int PPP = 256 / LP;       // positions per pass
+    constexpr int PP = 4;               // passes per round
+    constexpr int OPT = (G * HD + 255) / 256;   // outputs per thread
     __shared__ float qs[G * HD];
-    __shared__ float sc[G * TILE];
-    __shared__ float mrun[G], lrun[G], fac[G];
-    extern __shared__ float red[];      // [PG][G][HD]
+    __shared__ float att_m[PPP][G];
+    __shared__ float att_l[PPP][G];
+    extern __shared__ float att_o[];    // [PPP][G][HD]
 
     const int kvh = blockIdx.x, t = blockIdx.y;
     const int nq = nkv * G;
     const int L = st->pos + t + 1;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x;
     const int kvd = nkv * HD;
+    const int pl = tid / LP, dl = tid % LP;
     const float scale = 1.0f / sqrtf((float)HD);
     for (int i = tid; i < G * HD; i += 256) qs[i] = q[(size_t)t * nq * HD + (size_t)kvh * G * HD + i];
-    if (tid < G) { mrun[tid] = -1e30f; lrun[tid] = 0.0f; }
     __syncthreads();
-
-    const int dsub = tid % LP, pg = tid / LP;
-    float acc[G][8];
+    float qr[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
+        for (int e = 0; e < 8; e++) qr[g][e] = qs[g * HD + dl * 8 + e];
 
-    for (int p0 = 0; p0 < L; p0 += TILE) {
-        const int n = min(TILE, L - p0);
-        {
-            const int sub = lane % LP, slot = lane / LP;
-            const int pi = wave * PPW + slot;
-            const bool act = pi < n;
-            uint4 kv = make_uint4(0, 0, 0, 0);
-            if (act) kv = *reinterpret_cast<const uint4*>(kc + (size_t)(p0 + pi) * kvd + kvh * HD + sub * 8);
-            const half2_t k01 = as_h2(kv.x), k23 = as_h2(kv.y), k45 = as_h2(kv.z), k67 = as_h2(kv.w);
+    float runM[OPT], runL[OPT], runO[OPT];
+#pragma unroll
+    for (int j = 0; j < OPT; j++) { runM[j] = -INFINITY; runL[j] = 0.0f; runO[j] = 0.0f; }
+
+    for (int r0 = 0; r0 < L; r0 += PP * PPP) {
+        uint4 kk[PP], vv[PP];
+#pragma unroll
+        for (int qq = 0; qq < PP; qq++) {
+            const int p = r0 + qq * PPP + pl;
+            const int pc = p < L ? p : 0;
+            kk[qq] = *reinterpret_cast<const uint4*>(kc + (size_t)pc * kvd + kvh * HD + dl * 8);
+            vv[qq] = *reinterpret_cast<const uint4*>(vc + (size_t)pc * kvd + kvh * HD + dl * 8);
+        }
+        float sc[PP][G], mx[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) mx[g] = -INFINITY;
+#pragma unroll
+        for (int qq = 0; qq < PP; qq++) {
+            const half2_t k01 = as_h2(kk[qq].x), k23 = as_h2(kk[qq].y), k45 = as_h2(kk[qq].z),
+                          k67 = as_h2(kk[qq].w);
+            const float kf[8] = {(float)k01.x, (float)k01.y, (float)k23.x, (float)k23.y,
+                                 (float)k45.x, (float)k45.y, (float)k67.x, (float)k67.y};
+            const bool valid = r0 + qq * PPP + pl < L;
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float* qq = qs + g * HD + sub * 8;
-                float pd = qq[0] * (float)k01.x;
-                pd = pd + qq[1] * (float)k01.y;
-                pd = pd + qq[2] * (float)k23.x;
-                pd = pd + qq[3] * (float)k23.y;
-                pd = pd + qq[4] * (float)k45.x;
-                pd = pd + qq[5] * (float)k45.y;
-                pd = pd + qq[6] * (float)k67.x;
-                pd = pd + qq[7] * (float)k67.y;
-                pd = group_sum(pd, LP);
-                if (act && sub == 0) sc[g * TILE + pi] = pd * scale;
+                const float* qh = qr[g];
+                float sv = ((qh[0] * kf[0] + qh[1] * kf[1]) + (qh[2] * kf[2] + qh[3] * kf[3])) +
+                           ((qh[4] * kf[4] + qh[5] * kf[5]) + (qh[6] * kf[6] + qh[7] * kf[7]));
+                sv = lanes_sum<LP>(sv) * scale;
+                sc[qq][g] = valid ? sv : -INFINITY;
+                mx[g] = fmaxf(mx[g], sc[qq][g]);
             }
         }
+        if (dl == 0)
+#pragma unroll
+            for (int g = 0; g < G; g++) att_m[pl][g] = mx[g];
         __syncthreads();
-        if (wave == 0) {
-            for (int g = 0; g < G; g++) {
-                float m = lane < n ? sc[g * TILE + lane] : -1e30f;
-                m = wave_max(m);
-                const float mnew = fmaxf(mrun[g], m);
-                float e = 0.0f;
-                if (lane < n) {
-                    e = expf(sc[g * TILE + lane] - mnew);
-                    sc[g * TILE + lane] = e;
-                }
-                const float lsum = wave_sum(e);
-                if (lane == 0) {
-                    const float f = expf(mrun[g] - mnew);
-                    fac[g] = f;
-                    lrun[g] = lrun[g] * f + lsum;
-                    mrun[g] = mnew;
-                }
-            }
+        float Mr[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float v = att_m[0][g];
+            for (int i = 1; i < PPP; i++) v = fmaxf(v, att_m[i][g]);
+            Mr[g] = v;
         }
-        __syncthreads();
+        float ls[G], o[G][8];
 #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++) {
+            ls[g] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] * fac[g];
-        for (int pi = pg; pi < n; pi += PG) {
-            const uint4 vv = *reinterpret_cast<const uint4*>(vc + (size_t)(p0 + pi) * kvd + kvh * HD + dsub * 8);
-            const half2_t v01 = as_h2(vv.x), v23 = as_h2(vv.y), v45 = as_h2(vv.z), v67 = as_h2(vv.w);
+            for (int e = 0; e < 8; e++) o[g][e] = 0.0f;
+        }
+#pragma unroll
+        for (int qq = 0; qq < PP; qq++) {
+            const half2_t v01 = as_h2(vv[qq].x), v23 = as_h2(vv[qq].y), v45 = as_h2(vv[qq].z),
+                          v67 = as_h2(vv[qq].w);
             const float vf[8] = {(float)v01.x, (float)v01.y, (float)v23.x, (float)v23.y,
                                  (float)v45.x, (float)v45.y, (float)v67.x, (float)v67.y};
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                const float p = sc[g * TILE + pi];
+                const float p = sc[qq][g] == -INFINITY ? 0.0f : expf(sc[qq][g] - Mr[g]);
+                ls[g] = ls[g] + p;
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] + vf[e] * p;
+                for (int e = 0; e < 8; e++) o[g][e] = o[g][e] + p * vf[e];
             }
         }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) att_o[(pl * G + g) * HD + dl * 8 + e] = o[g][e];
+            if (dl == 0) att_l[pl][g] = ls[g];
+        }
         __syncthreads();
+#pragma unroll
+        for (int j = 0; j < OPT; j++) {
+            const int oi = tid + 256 * j;
+            if (oi < G * HD) {
+                const int g = oi / HD, d = oi % HD;
+                float Ox = 0.0f, Lx = 0.0f;
+                for (int i = 0; i < PPP; i++) {
+                    Ox = Ox + att_o[(i * G + g) * HD + d];
+                    Lx = Lx + att_l[i][g];
+                }
+                const float M2 = Mr[g];
+                const float Mn = fmaxf(runM[j], M2);
+                if (Mn != -INFINITY) {
+                    const float a = runM[j] == -INFINITY ? 0.0f : expf(runM[j] - Mn);
+                    const float b = M2 == -INFINITY ? 0.0f : expf(M2 - Mn);
+                    runL[j] = runL[j] * a + Lx * b;
+                    runO[j] = runO[j] * a + Ox * b;
+                    runM[j] = Mn;
+                }
+            }
+        }
+        __syncthreads();   // att_* are rewritten by the next round
     }
 #pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) red[(pg * G + g) * HD + dsub * 8 + e] = acc[g][e];
-    __syncthreads();
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        float s = 0.0f;
-        for (int k = 0; k < PG; k++) s += red[(k * G + g) * HD + d];
-        out16[(size_t)t * nq * HD + (size_t)(kvh * G + g) * HD + d] = f32_to_f16_bits(s / lrun[g]);
+    for (int j = 0; j < OPT; j++) {
+        const int oi = tid + 256 * j;
+        if (oi < G * HD) {
+            const int g = oi / HD, d = oi % HD;
+            out16[(size_t)t * nq * HD + (size_t)(kvh * G + g) * HD + d] = f32_to_f16_bits(runO[j] / runL[j]);
+        }
     }
 }
 
@@ -394,44 +522,72 @@ int mdx_launch_to_f16(const float* x, int n, uint16_t* x16, void* stream) {
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-size_t mdx_gemm_scratch_floats(int M, int N, int K) {
-    (void)M;
-    int cps;
-    const int ns = plan_splits(N, K, &cps);
-    return (size_t)ns * kMaxM * N;
+static int gemm_tiles(int N, int swiglu) {
+    return swiglu ? (N / 2 + kNT / 2 - 1) / (kNT / 2) : (N + kNT - 1) / kNT;
 }
 
-int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
-                    float* scratch, void* stream) {
-    if (M <= 0 || M > kMaxM || w->K % 32 != 0) return -1;
+// K splits of a residual projection: about 256 blocks in all, at least two
+// K-blocks of the widest kind per split.
+static int residual_splits(int N, int K) {
+    const int tiles = gemm_tiles(N, 0);
+    int ns = (256 + tiles - 1) / tiles;
+    const int max_ns = K / 256 > 0 ? K / 256 : 1;
+    if (ns > max_ns) ns = max_ns;
+    if (ns > kMaxSplits) ns = kMaxSplits;
+    return ns < 1 ? 1 : ns;
+}
+
+size_t mdx_gemm_scratch_floats(int M, int N, int K) {
+    (void)M;
+    return (size_t)residual_splits(N, K) * kMaxM * N;
+}
+
+static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
+                       float* part, int ns, void* stream) {
+    const int kb = w->kind == MDX_W_F16 ? 32 : (w->kind == MDX_W_I8 ? 64 : 128);
+    if (M <= 0 || M > kMaxM || w->K % kb != 0) return -1;
+    // exactly one destination: split partials, or the epilogue's output
+    if (part ? (ns < 1 || out != nullptr) : (ns != 1 || out == nullptr)) return -1;
     if (epilogue == 2 && w->N % 2) return -1;
-    if (w->kind == MDX_W_I4 && w->K % kKC != 0) return -1;   // int4 pieces are whole 16-byte words
-    int cps;
-    const int ns = plan_splits(w->N, w->K, &cps);
-    dim3 grid((w->N + kNT - 1) / kNT, ns);
+    dim3 grid(gemm_tiles(w->N, epilogue == 2), ns);
+    dim3 block(kGemmWaves * 64);
     const uint8_t* wp = (const uint8_t*)w->w;
+    float* of = (float*)out;
+    uint16_t* oh = (uint16_t*)out;
     switch (w->kind) {
         case MDX_W_F16:
-            hipLaunchKernelGGL(k_gemm<MDX_W_F16>, grid, dim3(256), 0, (hipStream_t)stream, x16, M, wp,
-                               w->K, w->N, cps, scratch);
+            hipLaunchKernelGGL(k_gemm<MDX_W_F16>, grid, block, 0, (hipStream_t)stream, x16, M, wp, w->K,
+                               w->N, w->scale, epilogue, of, oh, part);
             break;
         case MDX_W_I8:
-            hipLaunchKernelGGL(k_gemm<MDX_W_I8>, grid, dim3(256), 0, (hipStream_t)stream, x16, M, wp,
-                               w->K, w->N, cps, scratch);
+            hipLaunchKernelGGL(k_gemm<MDX_W_I8>, grid, block, 0, (hipStream_t)stream, x16, M, wp, w->K,
+                               w->N, w->scale, epilogue, of, oh, part);
             break;
         case MDX_W_I4:
-            hipLaunchKernelGGL(k_gemm<MDX_W_I4>, grid, dim3(256), 0, (hipStream_t)stream, x16, M, wp,
-                               w->K, w->N, cps, scratch);
+            hipLaunchKernelGGL(k_gemm<MDX_W_I4>, grid, block, 0, (hipStream_t)stream, x16, M, wp, w->K,
+                               w->N, w->scale, epilogue, of, oh, part);
             break;
         default:
             return -5;
     }
-    if (hipGetLastError() != hipSuccess) return -4;
-    const int cols = epilogue == 2 ? w->N / 2 : w->N;
-    int blocks = (M * cols + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(k_gemm_reduce, dim3(blocks), dim3(256), 0, (hipStream_t)stream, scratch, ns, M,
-                       w->N, w->scale, epilogue, (float*)out, (uint16_t*)out);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
+                    float* scratch, void* stream) {
+    (void)scratch;
+    return gemm_launch(x16, M, w, epilogue, out, nullptr, 1, stream);
+}
+
+int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w, float* hidden,
+                                  const float* norm_w, float eps, uint16_t* x16_out, float* scratch,
+                                  void* stream) {
+    if (w->N % 4) return -1;   // float4 rows in k_residual_norm
+    const int ns = residual_splits(w->N, w->K);
+    int rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_residual_norm, dim3(M), dim3(256), 0, (hipStream_t)stream, scratch, ns, w->N,
+                       w->scale, hidden, norm_w, eps, x16_out);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -453,8 +609,8 @@ int mdx_launch_attn_prefill(const mdx_state* state, const float* q, int M,
     if (nkv <= 0 || nq % nkv || M <= 0) return -1;
     const int G = nq / nkv;
     const int LP = hd / 8;
-    const int PG = 256 / (LP > 0 ? LP : 1);
-    const size_t lds = (size_t)PG * G * hd * 4;
+    const int PPP = 256 / (LP > 0 ? LP : 1);
+    const size_t lds = (size_t)PPP * G * hd * 4;
     if (lds > 48 * 1024) return -5;
     dim3 grid(nkv, M);
 #define MDX_PATTN(HD_, G_)                                                                          \

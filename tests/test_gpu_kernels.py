@@ -160,9 +160,9 @@ def test_attention_decode_fused(mdx, gpu, oracle_lib, pos, style):
 
 
 @pytest.mark.parametrize("S,M", [(0, 60), (0, 1), (100, 33), (4000, 64)])
-def test_attention_prefill(mdx, gpu, oracle_lib, S, M):
-    rng = np.random.default_rng(S + M)
-    nq, nkv, hd = 16, 8, 128
+@pytest.mark.parametrize("nq,nkv,hd", [(16, 8, 128), (8, 2, 64), (4, 2, 256)])
+def test_attention_prefill(mdx, gpu, oracle_lib, S, M, nq, nkv, hd):
+    rng = np.random.default_rng(S + M + hd)
     kvd = nkv * hd
     q = rng.standard_normal(M * nq * hd).astype(np.float32)
     k, v = _kv(rng, S + M, kvd)
