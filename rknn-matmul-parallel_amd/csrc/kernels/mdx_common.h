@@ -79,6 +79,36 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Lanes 0..31 only (lanes 32..63 are ignored), returned to every lane.
+__device__ __forceinline__ float half_sum_dpp(float v) {
+    v = row_sum16(v);
+    v = v + dpp<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+}
+__device__ __forceinline__ float half_max_dpp(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp<0x142, 0xA>(v));   // row 1 (read below) takes row 0's maximum
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+}
+// Sum / maximum over the four 16-lane rows of a wave, per column (lane & 15),
+// returned to every lane: the gfx950 row swaps (odd rows of one operand with
+// even rows of the other; upper half with lower half) run on the VALU.
+__device__ __forceinline__ float rows_sum4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+__device__ __forceinline__ float rows_max4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

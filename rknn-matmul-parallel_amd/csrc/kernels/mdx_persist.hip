@@ -116,6 +116,21 @@ __device__ __forceinline__ void ll_put_f32(unsigned* xb, int word, float v, unsi
     ll_put(xb, word + 1, u >> 16, ep);
 }
 
+// Four LL words in one 16-byte store (each word still carries its own epoch,
+// so a reader never accepts a partly written group).
+__device__ __forceinline__ void ll_put4(__amdgpu_buffer_rsrc_t rs, int word, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, word * 4, 0, 16);
+}
+__device__ __forceinline__ u32x4 ll_pack2(float v0, float v1, unsigned ep) {
+    const unsigned x = __float_as_uint(v0), y = __float_as_uint(v1), e = ep << 16;
+    u32x4 r;
+    r.x = (x & 0xffffu) | e;
+    r.y = (x >> 16) | e;
+    r.z = (y & 0xffffu) | e;
+    r.w = (y >> 16) | e;
+    return r;
+}
+
 // Polls N 16-byte groups until every word carries epoch ep.  Returns false
 // after kSpinLimit rounds (the data is then stale; the caller stops waiting).
 template <int N>
@@ -217,36 +232,87 @@ struct ChunkMajor {
     static constexpr bool RAGGED = CPR % STEP != 0;
 };
 
+// The value of the partner lane at distance O (a symmetric pairing that
+// flips lane bit log2(O) and keeps the higher bits): DPP within a 16-lane
+// row, the gfx950 row swaps across rows.
+template <int O>
+__device__ __forceinline__ float partner(float v) {
+    if constexpr (O == 1) return dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+    else if constexpr (O == 2) return dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    else if constexpr (O == 4) return dpp<0x141>(v);  // row_half_mirror: i <-> 7-i
+    else return dpp<0x128>(v);                        // row_ror:8 (i <-> i^8)
+}
+
+// One butterfly step at distance O over nv live values: the lane with bit O
+// clear keeps the low half, its partner the high half; each adds the other's
+// copy of the half it keeps.
+template <int O, int NV>
+__device__ __forceinline__ void rs_step(float (&v)[NV], int nv, int lane) {
+    const int half = nv / 2;
+    if constexpr (O >= 16) {
+        // row swaps: (lo, hi) -> (own lo, partner lo) below, (partner hi, own hi) above
+#pragma unroll
+        for (int k = 0; k < NV / 2; k++) {
+            if (k < half) {
+                if constexpr (O == 32) {
+                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]),
+                                                                    __float_as_uint(v[k + half]), false, false);
+                    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                } else {
+                    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]),
+                                                                    __float_as_uint(v[k + half]), false, false);
+                    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                }
+            }
+        }
+    } else {
+        // bitwise select: keeps both reads static (a select of two array
+        // elements would otherwise become a dynamically indexed read)
+        const unsigned up = (lane & O) ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int k = 0; k < NV / 2; k++) {
+            if (k < half) {
+                const unsigned lo = __float_as_uint(v[k]), hi = __float_as_uint(v[k + half]);
+                const float send = __uint_as_float((lo & up) | (hi & ~up));
+                const float keep = __uint_as_float((hi & up) | (lo & ~up));
+                v[k] = keep + partner<O>(send);
+            }
+        }
+    }
+}
+template <int O>
+__device__ __forceinline__ float sum_step(float v) {
+    if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        return v + partner<O>(v);
+    }
+}
+
 // Reduce-scatter of NV per-lane values over aligned groups of G lanes: on
 // return lane l holds the group total of value (l % G) / (G / NV).
 constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
 
+template <int NV, int G, int O = G / 2>
+__device__ __forceinline__ float reduce_scatter_from(float (&v)[NV], int nv, int lane) {
+    if constexpr (O == 0) {
+        return v[0];
+    } else {
+        if (nv > 1) {
+            rs_step<O, NV>(v, nv, lane);
+            return reduce_scatter_from<NV, G, O / 2>(v, nv / 2, lane);
+        }
+        v[0] = sum_step<O>(v[0]);
+        return reduce_scatter_from<NV, G, O / 2>(v, 1, lane);
+    }
+}
 template <int NV, int G>
 __device__ __forceinline__ float reduce_scatter(float (&v)[NV], int lane) {
-    constexpr int STEPS = ilog2(G);
-#pragma unroll
-    for (int st = 0; st < STEPS; st++) {
-        const int o = G >> (st + 1);
-        const int nv = NV >> st;
-        if (nv > 1) {
-            const int half = nv / 2;
-            // bitwise select: keeps both reads static (a select of two array
-            // elements would otherwise become a dynamically indexed read)
-            const unsigned up = (lane & o) ? 0xffffffffu : 0u;
-#pragma unroll
-            for (int k = 0; k < NV / 2; k++) {
-                if (k < half) {
-                    const unsigned lo = __float_as_uint(v[k]), hi = __float_as_uint(v[k + half]);
-                    const float send = __uint_as_float((lo & up) | (hi & ~up));
-                    const float keep = __uint_as_float((hi & up) | (lo & ~up));
-                    v[k] = keep + __shfl_xor(send, o, 64);
-                }
-            }
-        } else {
-            v[0] += __shfl_xor(v[0], o, 64);
-        }
-    }
-    return v[0];
+    return reduce_scatter_from<NV, G>(v, NV, lane);
 }
 
 // Row-major dot + reduction; red[r * NSPLIT + part] receives the row sums.
@@ -310,8 +376,11 @@ __device__ __forceinline__ void cm_dot(const uint4 (&w)[NWT], const uint4* xs4, 
         const int kc = t / R + S::STEP * i;
         if (!S::RAGGED || kc < S::CPR) acc = wdot<KIND>(w[i], xs4 + kc * XC, acc);
     }
-#pragma unroll
-    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    static_assert(R == 4, "the row rotations below sum the lanes equal mod 4");
+    acc = acc + dpp<0x124>(acc);   // row_ror:4
+    acc = acc + dpp<0x128>(acc);   // row_ror:8
+    acc = sum_step<16>(acc);
+    acc = sum_step<32>(acc);
     const int lane = t & 63;
     if (lane < R) red[(t >> 6) * R + lane] = acc;
 }
@@ -383,12 +452,17 @@ __device__ __forceinline__ void h8_to_f32(uint4 u, float (&f)[8]) {
     f[4] = (float)c.x; f[5] = (float)c.y; f[6] = (float)d.x; f[7] = (float)d.y;
 }
 
+// 2^x for x <= 0 (one v_exp_f32).  Scores are kept in the log2 domain, so the
+// softmax numerators are exp2(s - max).
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Online-softmax merge in the log2 domain: (m, l, o) absorbs (m2, l2, o2).
 __device__ __forceinline__ void ml_merge(float& m, float& l, float* o, int n, float m2, float l2,
                                          const float* o2) {
     const float M = fmaxf(m, m2);
     if (M == -INFINITY) return;
-    const float a = m == -INFINITY ? 0.0f : expf(m - M);
-    const float b = m2 == -INFINITY ? 0.0f : expf(m2 - M);
+    const float a = m == -INFINITY ? 0.0f : exp2_fast(m - M);
+    const float b = m2 == -INFINITY ? 0.0f : exp2_fast(m2 - M);
     l = l * a + l2 * b;
     for (int e = 0; e < n; e++) o[e] = o[e] * a + o2[e] * b;
     m = M;
@@ -412,11 +486,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     __shared__ float q_s[2 * HD];
     __shared__ float kn_s[HD];
     __shared__ float vn_s[HD];
-    __shared__ float att_o[16][2][HD];
-    __shared__ float att_m[16][2];
-    __shared__ float att_l[16][2];
-    __shared__ float cm_m[32], cm_l[32], cm_w[32];
-    __shared__ float cm_o[32][8];
+    __shared__ float att_o[4][2][HD];
+    __shared__ float att_m[4][2];
+    __shared__ float att_l[4][2];
     __shared__ unsigned long long bkey[4];
 
     const int t = threadIdx.x, b = blockIdx.x, lane = t & 63, wave = t >> 6;
@@ -565,8 +637,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         MDX_TRACE(16 * l + 12);
-        // Scores of all passes first (independent chains), one workgroup-wide
-        // max per head, then P.V summed over the 16 position groups in LDS.
+        // Scores of all passes first (independent chains), then per wave: the
+        // maximum, the softmax numerators and P.V summed over its four
+        // position rows; the four waves are merged through LDS.
         // (runM, runL, runO) of thread t: head t >> 7, dimension t & 127.
         float runM = -INFINITY, runL = 0.0f, runO = 0.0f;
         {
@@ -579,6 +652,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 float sc[PP][2], vf[PP][8];
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
+                    sc[qq][0] = -INFINITY;
+                    sc[qq][1] = -INFINITY;
+                    if (16 * (q0 + qq) >= n) continue;   // the whole pass lies past the chunk
                     const int pi = 16 * (q0 + qq) + pl;
                     const bool isnew = pi < n && p0 + pi == pos;
                     float kf[8];
@@ -595,65 +671,74 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 #pragma unroll
                     for (int hh = 0; hh < 2; hh++) {
                         const float* qh = q[hh];
-                        sc[qq][hh] = ((qh[0] * kf[0] + qh[1] * kf[1]) + (qh[2] * kf[2] + qh[3] * kf[3])) +
-                                     ((qh[4] * kf[4] + qh[5] * kf[5]) + (qh[6] * kf[6] + qh[7] * kf[7]));
+                        float acc = qh[0] * kf[0];
+#pragma unroll
+                        for (int e = 1; e < 8; e++) acc = fmaf(qh[e], kf[e], acc);
+                        // log2(e) / sqrt(128): scores in the log2 domain
+                        const float v = row_sum16(acc) * 0.12751743074924928f;
+                        sc[qq][hh] = pi < n ? v : -INFINITY;
                     }
                 }
                 float mx[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-                for (int qq = 0; qq < PP; qq++) {
-                    const bool valid = 16 * (q0 + qq) + pl < n;
+                for (int qq = 0; qq < PP; qq++)
 #pragma unroll
-                    for (int hh = 0; hh < 2; hh++) {
-                        const float v = row_sum16(sc[qq][hh]) * 0.08838834764831845f;   // 1/sqrt(128)
-                        sc[qq][hh] = valid ? v : -INFINITY;
-                        mx[hh] = fmaxf(mx[hh], sc[qq][hh]);
-                    }
-                }
+                    for (int hh = 0; hh < 2; hh++) mx[hh] = fmaxf(mx[hh], sc[qq][hh]);
                 if (q0 == 0) MDX_TRACE(16 * l + 14);
-                if (dl == 0) {
-                    att_m[pl][0] = mx[0];
-                    att_m[pl][1] = mx[1];
-                }
-                __syncthreads();
-                float M[2];
+                // softmax numerators against this wave's maximum; the four
+                // position rows of the wave summed on the VALU
+                float Mw[2], ls[2] = {0.0f, 0.0f}, o[2][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
-                    float v = att_m[0][hh];
-#pragma unroll
-                    for (int i = 1; i < 16; i++) v = fmaxf(v, att_m[i][hh]);
-                    M[hh] = v;
-                }
-                float ls[2] = {0.0f, 0.0f}, o[2][8];
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++)
+                    Mw[hh] = rows_max4(mx[hh]);
 #pragma unroll
                     for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
+                }
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
+                    if (16 * (q0 + qq) >= n) continue;
 #pragma unroll
                     for (int hh = 0; hh < 2; hh++) {
-                        const float p = sc[qq][hh] == -INFINITY ? 0.0f : expf(sc[qq][hh] - M[hh]);
+                        const float p = sc[qq][hh] == -INFINITY ? 0.0f : exp2_fast(sc[qq][hh] - Mw[hh]);
                         ls[hh] = ls[hh] + p;
 #pragma unroll
-                        for (int e = 0; e < 8; e++) o[hh][e] = o[hh][e] + p * vf[qq][e];
+                        for (int e = 0; e < 8; e++) o[hh][e] = fmaf(p, vf[qq][e], o[hh][e]);
                     }
                 }
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
+                    ls[hh] = rows_sum4(ls[hh]);
 #pragma unroll
-                    for (int e = 0; e < 8; e++) att_o[pl][hh][dl * 8 + e] = o[hh][e];
-                    if (dl == 0) att_l[pl][hh] = ls[hh];
+                    for (int e = 0; e < 8; e++) o[hh][e] = rows_sum4(o[hh][e]);
+                }
+                if (lane < 16) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) att_o[wave][hh][dl * 8 + e] = o[hh][e];
+                    if (lane == 0) {
+#pragma unroll
+                        for (int hh = 0; hh < 2; hh++) {
+                            att_m[wave][hh] = Mw[hh];
+                            att_l[wave][hh] = ls[hh];
+                        }
+                    }
                 }
                 __syncthreads();
+                // thread t: head t >> 7, dimension t & 127; the four waves merged
                 const int hh = t >> 7, d = t & 127;
+                float Mx = att_m[0][hh];
+#pragma unroll
+                for (int w = 1; w < 4; w++) Mx = fmaxf(Mx, att_m[w][hh]);
                 float Ox = 0.0f, Lx = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    Ox = Ox + att_o[i][hh][d];
-                    Lx = Lx + att_l[i][hh];
+                for (int w = 0; w < 4; w++) {
+                    const float mw = att_m[w][hh];
+                    const float f = mw == -INFINITY ? 0.0f : exp2_fast(mw - Mx);
+                    Ox = Ox + att_o[w][hh][d] * f;
+                    Lx = Lx + att_l[w][hh] * f;
                 }
-                ml_merge(runM, runL, &runO, 1, M[hh], Lx, &Ox);
+                ml_merge(runM, runL, &runO, 1, Mx, Lx, &Ox);
                 __syncthreads();   // att_* are rewritten by the next round
             };
             round(kr, vr, 0);
@@ -672,73 +757,87 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         MDX_TRACE(16 * l + 13);
         {
+            // 16-byte stores: thread t < 128 writes values 2t and 2t+1
             const int hh = t >> 7, d = t & 127;
             const int base = W_PART + (j * GRP + s) * PART_WORDS;
-            ll_put_f32(xb, base + 8 + 256 * hh + 2 * d, runO, ep);
-            if (d == 0) {
-                ll_put_f32(xb, base + 4 * hh, runM, ep);
-                ll_put_f32(xb, base + 4 * hh + 2, runL, ep);
-            }
+            float* po = &att_o[0][0][0];
+            po[t] = runO;
+            __syncthreads();
+            if (t < 128) ll_put4(rs, base + 8 + 4 * t, ll_pack2(po[2 * t], po[2 * t + 1], ep));
+            if (d == 0) ll_put4(rs, base + 4 * hh, ll_pack2(runM, runL, ep));
         }
         MDX_TRACE(16 * l + 4);
 
-        // ================= C: merge the 32 partials of KV head j ==========
-        {
-            const int hh = s >> 4, d0 = (s & 15) * 8;
-            bool ok = true;
-            if (t < 32) {
-                const int base = W_PART + (j * GRP + t) * PART_WORDS;
-                int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0,
-                             base + 12 + 256 * hh + 2 * d0, base + 16 + 256 * hh + 2 * d0,
-                             base + 20 + 256 * hh + 2 * d0};
-                u32x4 v[5];
-                ok = ll_wait<5>(rs, wd, v, ep, dead);
-                cm_m[t] = ll_f32(v[0].x, v[0].y);
-                cm_l[t] = ll_f32(v[0].z, v[0].w);
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    cm_o[t][2 * k] = ll_f32(v[1 + k].x, v[1 + k].y);
-                    cm_o[t][2 * k + 1] = ll_f32(v[1 + k].z, v[1 + k].w);
-                }
-            }
-            if (__syncthreads_or(!ok)) dead = true;
+        // Waves 1..3 request their remaining gate/up and down weights now; wave 0
+        // does so after the merge, so that nothing queues in front of its poll.
+        uint4 wF[SF::NW];
+        if (wave != 0) {
             rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
-            if (t < 32) {
-                float M = cm_m[0];
+            cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
+        }
+
+        // ================= C: merge the 32 partials of KV head j (wave 0) ==========
+        // lane i < 32 holds split i; lanes 32..63 poll the same words and add nothing
+        if (wave == 0) {
+            const int hh = s >> 4, d0 = (s & 15) * 8;
+            const int i = lane & 31;
+            const int base = W_PART + (j * GRP + i) * PART_WORDS;
+            int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0, base + 12 + 256 * hh + 2 * d0,
+                         base + 16 + 256 * hh + 2 * d0, base + 20 + 256 * hh + 2 * d0};
+            u32x4 v[5];
+            if (!ll_wait<5>(rs, wd, v, ep, dead)) dead = true;
+            const bool mine = lane < 32;
+            const float m = mine ? ll_f32(v[0].x, v[0].y) : -INFINITY;
+            const float M = half_max_dpp(m);
+            const float w = m == -INFINITY ? 0.0f : exp2_fast(m - M);
+            const float Ls = half_sum_dpp(mine ? ll_f32(v[0].z, v[0].w) * w : 0.0f);
+            float O[8];
 #pragma unroll
-                for (int i = 1; i < 32; i++) M = fmaxf(M, cm_m[i]);
-                const float m = cm_m[t];
-                cm_w[t] = m == -INFINITY ? 0.0f : expf(m - M);
+            for (int k = 0; k < 4; k++) {
+                O[2 * k] = half_sum_dpp(mine ? ll_f32(v[1 + k].x, v[1 + k].y) * w : 0.0f);
+                O[2 * k + 1] = half_sum_dpp(mine ? ll_f32(v[1 + k].z, v[1 + k].w) * w : 0.0f);
             }
-            __syncthreads();
-            if (t < 8) {
-                float Ls = 0.0f, O = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 32; i++) {
-                    const float w = cm_w[i];
-                    Ls = Ls + cm_l[i] * w;
-                    O = O + cm_o[i][t] * w;
-                }
-                ll_put(xb, W_ATT + (2 * j + hh) * HD + d0 + t, f32_to_f16_bits(O / Ls), ep);
+            if (lane < 2) {
+                const unsigned e = ep << 16;
+                u32x4 pk;
+                const bool hi = lane == 1;
+                pk.x = f32_to_f16_bits((hi ? O[4] : O[0]) / Ls) | e;
+                pk.y = f32_to_f16_bits((hi ? O[5] : O[1]) / Ls) | e;
+                pk.z = f32_to_f16_bits((hi ? O[6] : O[2]) / Ls) | e;
+                pk.w = f32_to_f16_bits((hi ? O[7] : O[3]) / Ls) | e;
+                ll_put4(rs, W_ATT + (2 * j + hh) * HD + d0 + 4 * lane, pk);
             }
+        }
+        if (wave == 0) {
+            rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+            cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
         }
         MDX_TRACE(16 * l + 5);
 
         // ================= D: o projection + residual ==========
-        uint4 wF[SF::NW];
-        cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
         const float sclD = Ly.so ? Ly.so[4 * b + (t & 3)] : 1.0f;
         {
-            int wd[2] = {W_ATT + 8 * t, W_ATT + 8 * t + 4};
-            u32x4 v[2];
-            const bool ok = ll_wait<2>(rs, wd, v, ep, dead);
-            uint4 x;
-            x.x = (v[0].x & 0xffffu) | (v[0].y << 16);
-            x.y = (v[0].z & 0xffffu) | (v[0].w << 16);
-            x.z = (v[1].x & 0xffffu) | (v[1].y << 16);
-            x.w = (v[1].z & 0xffffu) | (v[1].w << 16);
-            xs4[t] = x;
-            if (__syncthreads_or(!ok)) dead = true;
+            // waves 1 and 2 gather the attention output (wave 0's weight
+            // requests were issued last)
+            bool ok = true;
+            if (wave == 1 || wave == 2) {
+                const int u = t - 64;
+                int wd[4] = {W_ATT + 16 * u, W_ATT + 16 * u + 4, W_ATT + 16 * u + 8, W_ATT + 16 * u + 12};
+                u32x4 v[4];
+                ok = ll_wait<4>(rs, wd, v, ep, dead);
+                uint4 x0, x1;
+                x0.x = (v[0].x & 0xffffu) | (v[0].y << 16);
+                x0.y = (v[0].z & 0xffffu) | (v[0].w << 16);
+                x0.z = (v[1].x & 0xffffu) | (v[1].y << 16);
+                x0.w = (v[1].z & 0xffffu) | (v[1].w << 16);
+                x1.x = (v[2].x & 0xffffu) | (v[2].y << 16);
+                x1.y = (v[2].z & 0xffffu) | (v[2].w << 16);
+                x1.z = (v[3].x & 0xffffu) | (v[3].y << 16);
+                x1.w = (v[3].z & 0xffffu) | (v[3].w << 16);
+                xs4[2 * u] = x0;
+                xs4[2 * u + 1] = x1;
+            }
+            if (__syncthreads_or(!ok || dead)) dead = true;   // wave 0 may have timed out in C
         }
         MDX_TRACE(16 * l + 6);
         cm_dot<KIND, 4, QD>(wD, xs4, red, t);
