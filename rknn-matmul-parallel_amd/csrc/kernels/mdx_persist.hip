@@ -55,10 +55,14 @@ constexpr int W_CTRL = 0;                          // [0] step counter
 constexpr int W_QKV = 16;                          // [NKV][512 values][2]
 constexpr int PART_WORDS = 520;                    // m0 l0 m1 l1 (x2) | o0[128] x2 | o1[128] x2
 constexpr int W_PART = W_QKV + NKV * 1024;         // [NKV][GRP][PART_WORDS]
-constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [QD] fp16
-constexpr int W_HO = W_ATT + QD;                   // [D][2] hidden after o
-constexpr int W_ACT = W_HO + 2 * D;                // [NB][16] fp16 (12 used: 64-byte slots)
-constexpr int W_HD = W_ACT + NB * 16;              // [D][2] hidden after down
+// The attention output and the SwiGLU activations are written in NREP
+// copies; workgroup b reads copy b % NREP, which spreads the all-to-all reads
+// of one exchange over more memory channels.
+constexpr int NREP = 4;
+constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [NREP][QD] fp16
+constexpr int W_HO = W_ATT + NREP * QD;            // [D][2] hidden after o
+constexpr int W_ACT = W_HO + 2 * D;                // [NREP][NB][16] fp16 (12 used: 64-byte slots)
+constexpr int W_HD = W_ACT + NREP * NB * 16;       // [D][2] hidden after down
 constexpr int W_AMAX = W_HD + 2 * D;               // [NB][4] argmax keys
 constexpr int W_TOTAL = W_AMAX + NB * 4;
 static_assert(W_PART % 4 == 0 && W_ATT % 4 == 0 && W_HO % 4 == 0 && W_ACT % 4 == 0 &&
@@ -797,15 +801,15 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 O[2 * k] = half_sum_dpp(mine ? ll_f32(v[1 + k].x, v[1 + k].y) * w : 0.0f);
                 O[2 * k + 1] = half_sum_dpp(mine ? ll_f32(v[1 + k].z, v[1 + k].w) * w : 0.0f);
             }
-            if (lane < 2) {
+            if (lane < 2 * NREP) {   // lane: copy lane / 2, half lane % 2
                 const unsigned e = ep << 16;
                 u32x4 pk;
-                const bool hi = lane == 1;
+                const bool hi = (lane & 1) == 1;
                 pk.x = f32_to_f16_bits((hi ? O[4] : O[0]) / Ls) | e;
                 pk.y = f32_to_f16_bits((hi ? O[5] : O[1]) / Ls) | e;
                 pk.z = f32_to_f16_bits((hi ? O[6] : O[2]) / Ls) | e;
                 pk.w = f32_to_f16_bits((hi ? O[7] : O[3]) / Ls) | e;
-                ll_put4(rs, W_ATT + (2 * j + hh) * HD + d0 + 4 * lane, pk);
+                ll_put4(rs, W_ATT + (lane >> 1) * QD + (2 * j + hh) * HD + d0 + 4 * (lane & 1), pk);
             }
         }
         if (wave == 0) {
@@ -822,7 +826,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             bool ok = true;
             if (wave == 1 || wave == 2) {
                 const int u = t - 64;
-                int wd[4] = {W_ATT + 16 * u, W_ATT + 16 * u + 4, W_ATT + 16 * u + 8, W_ATT + 16 * u + 12};
+                const int wb = W_ATT + (b % NREP) * QD + 16 * u;
+                int wd[4] = {wb, wb + 4, wb + 8, wb + 12};
                 u32x4 v[4];
                 ok = ll_wait<4>(rs, wd, v, ep, dead);
                 uint4 x0, x1;
@@ -879,9 +884,16 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             gu_s[t] = y * sclE;
         }
         __syncthreads();
-        if (t < 12) {
-            const float g = gu_s[t], u = gu_s[12 + t];
-            ll_put(xb, W_ACT + 16 * b + t, f32_to_f16_bits(silu_mul(g, u)), ep);
+        if (t < 3 * NREP) {
+            // lane t: copy t / 3, values 4 (t % 3) .. +3 in one 16-byte store
+            const int c = t % 3;
+            const unsigned e = ep << 16;
+            u32x4 pk;
+            pk.x = f32_to_f16_bits(silu_mul(gu_s[4 * c + 0], gu_s[12 + 4 * c + 0])) | e;
+            pk.y = f32_to_f16_bits(silu_mul(gu_s[4 * c + 1], gu_s[12 + 4 * c + 1])) | e;
+            pk.z = f32_to_f16_bits(silu_mul(gu_s[4 * c + 2], gu_s[12 + 4 * c + 2])) | e;
+            pk.w = f32_to_f16_bits(silu_mul(gu_s[4 * c + 3], gu_s[12 + 4 * c + 3])) | e;
+            ll_put4(rs, W_ACT + (t / 3) * (NB * 16) + 16 * b + 4 * c, pk);
         }
         MDX_TRACE(16 * l + 9);
 
@@ -889,7 +901,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         const float sclF = Ly.sdown ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
         MDX_TRACE(16 * l + 15);
         {
-            int wd[3] = {W_ACT + 16 * t, W_ACT + 16 * t + 4, W_ACT + 16 * t + 8};
+            const int wb = W_ACT + (b % NREP) * (NB * 16) + 16 * t;
+            int wd[3] = {wb, wb + 4, wb + 8};
             u32x4 v[3];
             const bool ok = ll_wait<3>(rs, wd, v, ep, dead);
             uint2* x2 = reinterpret_cast<uint2*>(xs4);
