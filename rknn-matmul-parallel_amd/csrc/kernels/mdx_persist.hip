@@ -158,6 +158,27 @@ __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&w
     }
 }
 
+// Polls the first group alone, then requests the others together.  For an
+// exchange whose writers finish over a spread of time this keeps one load per
+// thread in flight while waiting, which shortens the exchange (fewer requests
+// compete with the writes and with the other readers' polls).
+template <int N>
+__device__ __forceinline__ bool ll_wait_probe(__amdgpu_buffer_rsrc_t rs, const int (&word)[N],
+                                              u32x4 (&v)[N], unsigned ep, bool dead) {
+    int w0[1] = {word[0]};
+    u32x4 v0[1];
+    bool ok = ll_wait<1>(rs, w0, v0, ep, dead);
+    v[0] = v0[0];
+    int wr[N - 1];
+    u32x4 vr[N - 1];
+#pragma unroll
+    for (int i = 1; i < N; i++) wr[i - 1] = word[i];
+    ok = ll_wait<N - 1>(rs, wr, vr, ep, dead) && ok;
+#pragma unroll
+    for (int i = 1; i < N; i++) v[i] = vr[i - 1];
+    return ok;
+}
+
 // Layer pointers are computed, not loaded: a load of them would be a vector
 // memory load (the kernel writes global memory, so the compiler cannot use
 // scalar loads) and would queue behind the weight stream.
@@ -829,7 +850,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 const int wb = W_ATT + (b % NREP) * QD + 16 * u;
                 int wd[4] = {wb, wb + 4, wb + 8, wb + 12};
                 u32x4 v[4];
-                ok = ll_wait<4>(rs, wd, v, ep, dead);
+                ok = ll_wait_probe<4>(rs, wd, v, ep, dead);
                 uint4 x0, x1;
                 x0.x = (v[0].x & 0xffffu) | (v[0].y << 16);
                 x0.y = (v[0].z & 0xffffu) | (v[0].w << 16);
@@ -904,7 +925,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int wb = W_ACT + (b % NREP) * (NB * 16) + 16 * t;
             int wd[3] = {wb, wb + 4, wb + 8};
             u32x4 v[3];
-            const bool ok = ll_wait<3>(rs, wd, v, ep, dead);
+            const bool ok = ll_wait_probe<3>(rs, wd, v, ep, dead);
             uint2* x2 = reinterpret_cast<uint2*>(xs4);
 #pragma unroll
             for (int k = 0; k < 3; k++) {
