@@ -561,7 +561,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 
     // lm_head rows of this workgroup; the first batch is requested during the
     // last layer's gate/up stage
-    constexpr int U = 16;
+#ifndef MDX_LM_ROWS
+#define MDX_LM_ROWS 16
+#endif
+    constexpr int U = MDX_LM_ROWS;      // rows per wave batch (power of two, <= 64)
+    constexpr int PER = 64 / U;         // lanes holding one row's total
     const int rb = (int)(((long long)b * a.vocab) / NB);
     const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
     auto load_rows = [&](uint4 (&w)[U], float& sc, int base) {
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int r = min(base + u, re - 1);
             w[u] = *reinterpret_cast<const uint4*>(a.lm_w + (size_t)r * D + lane * 16);
         }
-        sc = a.lm_scale[min(base + (lane >> 2), re - 1)];
+        sc = a.lm_scale[min(base + lane / PER, re - 1)];
     };
     uint4 w0[U];
     float sc0 = 0.0f;
@@ -979,8 +983,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 #pragma unroll
             for (int u = 0; u < U; u++) v[u] = dot16_i8(w[u], x0, x1, 0.0f);
             const float tot = reduce_scatter<U, 64>(v, lane);
-            const int r = base + (lane >> 2);
-            if ((lane & 3) == 0 && r < re) {
+            const int r = base + lane / PER;
+            if ((lane % PER) == 0 && r < re) {
                 const float y = tot * sc;
                 a.logits[r] = y;
                 if (y == y) {
