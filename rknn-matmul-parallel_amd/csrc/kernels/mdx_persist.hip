@@ -481,18 +481,6 @@ __device__ __forceinline__ void h8_to_f32(uint4 u, float (&f)[8]) {
 // softmax numerators are exp2(s - max).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Online-softmax merge in the log2 domain: (m, l, o) absorbs (m2, l2, o2).
-__device__ __forceinline__ void ml_merge(float& m, float& l, float* o, int n, float m2, float l2,
-                                         const float* o2) {
-    const float M = fmaxf(m, m2);
-    if (M == -INFINITY) return;
-    const float a = m == -INFINITY ? 0.0f : exp2_fast(m - M);
-    const float b = m2 == -INFINITY ? 0.0f : exp2_fast(m2 - M);
-    l = l * a + l2 * b;
-    for (int e = 0; e < n; e++) o[e] = o[e] * a + o2[e] * b;
-    m = M;
-}
-
 // ---- the step kernel --------------------------------------------------------
 
 template <int KIND>
@@ -666,9 +654,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         MDX_TRACE(16 * l + 12);
-        // Scores of all passes first (independent chains), then per wave: the
-        // maximum, the softmax numerators and P.V summed over its four
-        // position rows; the four waves are merged through LDS.
+        // Online softmax per wave: each wave keeps one running maximum per head
+        // (shared by its four 16-lane position rows) and rescales its running
+        // sums when a round raises it.  After the last round the four rows are
+        // summed on the VALU and the four waves merged through LDS.
         // (runM, runL, runO) of thread t: head t >> 7, dimension t & 127.
         float runM = -INFINITY, runL = 0.0f, runO = 0.0f;
         {
@@ -677,6 +666,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             for (int hh = 0; hh < 2; hh++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) q[hh][e] = q_s[hh * HD + dl * 8 + e];
+            float Mw[2] = {-INFINITY, -INFINITY}, ls[2] = {0.0f, 0.0f}, o[2][8];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
             auto round = [&](const uint4 (&kk)[PP], const uint4 (&vv)[PP], int q0) {
                 float sc[PP][2], vf[PP][8];
 #pragma unroll
@@ -714,14 +708,16 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 #pragma unroll
                     for (int hh = 0; hh < 2; hh++) mx[hh] = fmaxf(mx[hh], sc[qq][hh]);
                 if (q0 == 0) MDX_TRACE(16 * l + 14);
-                // softmax numerators against this wave's maximum; the four
-                // position rows of the wave summed on the VALU
-                float Mw[2], ls[2] = {0.0f, 0.0f}, o[2][8];
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
-                    Mw[hh] = rows_max4(mx[hh]);
+                    const float Mn = fmaxf(Mw[hh], rows_max4(mx[hh]));   // uniform over the wave
+                    if (Mn != -INFINITY) {
+                        const float a = Mw[hh] == -INFINITY ? 0.0f : exp2_fast(Mw[hh] - Mn);
+                        ls[hh] = ls[hh] * a;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) o[hh][e] = 0.0f;
+                        for (int e = 0; e < 8; e++) o[hh][e] = o[hh][e] * a;
+                        Mw[hh] = Mn;
+                    }
                 }
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
@@ -734,55 +730,74 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                         for (int e = 0; e < 8; e++) o[hh][e] = fmaf(p, vf[qq][e], o[hh][e]);
                     }
                 }
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    ls[hh] = rows_sum4(ls[hh]);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) o[hh][e] = rows_sum4(o[hh][e]);
-                }
-                if (lane < 16) {
-#pragma unroll
-                    for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-                        for (int e = 0; e < 8; e++) att_o[wave][hh][dl * 8 + e] = o[hh][e];
-                    if (lane == 0) {
-#pragma unroll
-                        for (int hh = 0; hh < 2; hh++) {
-                            att_m[wave][hh] = Mw[hh];
-                            att_l[wave][hh] = ls[hh];
-                        }
-                    }
-                }
-                __syncthreads();
-                // thread t: head t >> 7, dimension t & 127; the four waves merged
-                const int hh = t >> 7, d = t & 127;
-                float Mx = att_m[0][hh];
-#pragma unroll
-                for (int w = 1; w < 4; w++) Mx = fmaxf(Mx, att_m[w][hh]);
-                float Ox = 0.0f, Lx = 0.0f;
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    const float mw = att_m[w][hh];
-                    const float f = mw == -INFINITY ? 0.0f : exp2_fast(mw - Mx);
-                    Ox = Ox + att_o[w][hh][d] * f;
-                    Lx = Lx + att_l[w][hh] * f;
-                }
-                ml_merge(runM, runL, &runO, 1, Mx, Lx, &Ox);
-                __syncthreads();   // att_* are rewritten by the next round
             };
-            round(kr, vr, 0);
-            for (int q0 = PP; 16 * q0 < n; q0 += PP) {      // chunks longer than 16*PP
-                uint4 kx[PP], vx[PP];
+            // chunks longer than 16*PP positions: with int8/int4 weights the rows
+            // of the next round are requested before the current round is
+            // computed (two register sets)
+            auto load_round = [&](uint4 (&kk)[PP], uint4 (&vv)[PP], int q0) {
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
                     const int pi = 16 * (q0 + qq) + pl;
                     const int p = p0 + pi;
                     const int pc = (pi < n && p != pos) ? p : 0;
-                    kx[qq] = *reinterpret_cast<const uint4*>(Ly.kc + (size_t)pc * KVD + j * HD + dl * 8);
-                    vx[qq] = *reinterpret_cast<const uint4*>(Ly.vc + (size_t)pc * KVD + j * HD + dl * 8);
+                    kk[qq] = *reinterpret_cast<const uint4*>(Ly.kc + (size_t)pc * KVD + j * HD + dl * 8);
+                    vv[qq] = *reinterpret_cast<const uint4*>(Ly.vc + (size_t)pc * KVD + j * HD + dl * 8);
                 }
-                round(kx, vx, q0);
+            };
+            uint4 kx[PP], vx[PP];
+            if constexpr (KIND != MDX_W_F16) {
+                if (16 * PP < n) load_round(kx, vx, PP);
+                round(kr, vr, 0);
+                for (int q0 = PP; 16 * q0 < n; q0 += 2 * PP) {
+                    if (16 * (q0 + PP) < n) load_round(kr, vr, q0 + PP);
+                    round(kx, vx, q0);
+                    if (16 * (q0 + PP) >= n) break;
+                    if (16 * (q0 + 2 * PP) < n) load_round(kx, vx, q0 + 2 * PP);
+                    round(kr, vr, q0 + PP);
+                }
+            } else {
+                // fp16 weights leave no registers for a second set: one round at a time
+                round(kr, vr, 0);
+                for (int q0 = PP; 16 * q0 < n; q0 += PP) {
+                    load_round(kx, vx, q0);
+                    round(kx, vx, q0);
+                }
             }
+
+            // the four position rows of each wave, then the four waves
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                ls[hh] = rows_sum4(ls[hh]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[hh][e] = rows_sum4(o[hh][e]);
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) att_o[wave][hh][dl * 8 + e] = o[hh][e];
+                if (lane == 0) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        att_m[wave][hh] = Mw[hh];
+                        att_l[wave][hh] = ls[hh];
+                    }
+                }
+            }
+            __syncthreads();
+            const int hh = t >> 7, d = t & 127;
+            float Mx = att_m[0][hh];
+#pragma unroll
+            for (int w = 1; w < 4; w++) Mx = fmaxf(Mx, att_m[w][hh]);
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float mw = att_m[w][hh];
+                const float f = mw == -INFINITY ? 0.0f : exp2_fast(mw - Mx);
+                runO = runO + att_o[w][hh][d] * f;
+                runL = runL + att_l[w][hh] * f;
+            }
+            runM = Mx;
+            __syncthreads();   // att_o is reused for the partial record below
         }
         MDX_TRACE(16 * l + 13);
         {
