@@ -55,15 +55,15 @@ constexpr int W_CTRL = 0;                          // [0] step counter
 constexpr int W_QKV = 16;                          // [NKV][512 values][2]
 constexpr int PART_WORDS = 520;                    // m0 l0 m1 l1 (x2) | o0[128] x2 | o1[128] x2
 constexpr int W_PART = W_QKV + NKV * 1024;         // [NKV][GRP][PART_WORDS]
-// The attention output and the SwiGLU activations are written in NREP
-// copies; workgroup b reads copy b % NREP, which spreads the all-to-all reads
-// of one exchange over more memory channels.
+// The all-to-all exchanges (attention output, hidden state after o and after
+// down, SwiGLU activations) are written in NREP copies; workgroup b reads copy
+// b % NREP, which spreads the reads of one exchange over more memory channels.
 constexpr int NREP = 4;
 constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [NREP][QD] fp16
-constexpr int W_HO = W_ATT + NREP * QD;            // [D][2] hidden after o
-constexpr int W_ACT = W_HO + 2 * D;                // [NREP][NB][16] fp16 (12 used: 64-byte slots)
-constexpr int W_HD = W_ACT + NREP * NB * 16;       // [D][2] hidden after down
-constexpr int W_AMAX = W_HD + 2 * D;               // [NB][4] argmax keys
+constexpr int W_HO = W_ATT + NREP * QD;            // [NREP][D][2] hidden after o
+constexpr int W_ACT = W_HO + NREP * 2 * D;         // [NREP][NB][16] fp16 (12 used: 64-byte slots)
+constexpr int W_HD = W_ACT + NREP * NB * 16;       // [NREP][D][2] hidden after down
+constexpr int W_AMAX = W_HD + NREP * 2 * D;        // [NB][4] argmax keys
 constexpr int W_TOTAL = W_AMAX + NB * 4;
 static_assert(W_PART % 4 == 0 && W_ATT % 4 == 0 && W_HO % 4 == 0 && W_ACT % 4 == 0 &&
               W_HD % 4 == 0 && W_AMAX % 4 == 0, "16-byte aligned regions");
@@ -133,6 +133,21 @@ __device__ __forceinline__ u32x4 ll_pack2(float v0, float v1, unsigned ep) {
     r.z = (y & 0xffffu) | e;
     r.w = (y >> 16) | e;
     return r;
+}
+
+// Wave 0: lanes 0..3 hold the workgroup's 4 hidden values; lanes 0..2*NREP-1
+// store them, two per 16-byte group, into every copy of the region at base.
+__device__ __forceinline__ void put_hidden4(__amdgpu_buffer_rsrc_t rs, int base, int b, float hv,
+                                            unsigned ep, int lane) {
+    const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv), 0));
+    const float v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv), 1));
+    const float v2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv), 2));
+    const float v3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hv), 3));
+    if (lane < 2 * NREP) {
+        const bool hi = (lane & 1) != 0;
+        ll_put4(rs, base + (lane >> 1) * (2 * D) + 8 * b + 4 * (lane & 1),
+                ll_pack2(hi ? v2 : v0, hi ? v3 : v1, ep));
+    }
 }
 
 // Polls N 16-byte groups until every word carries epoch ep.  Returns false
@@ -586,7 +601,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         const float rn1 = qknw ? qknw[ri1] : 1.0f;
         const float sclA = Ly.sqkv ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
         if (l > 0) {
-            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
+            const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
+            int wd[2] = {wb, wb + 4};
             u32x4 v[2];
             const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
@@ -887,9 +903,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * l + 6);
         cm_dot<KIND, 4, QD>(wD, xs4, red, t);
         __syncthreads();
-        if (t < 4) {
-            const float y = ((red[t] + red[4 + t]) + (red[8 + t] + red[12 + t])) * sclD;
-            ll_put_f32(xb, W_HO + 2 * (4 * b + t), hres[t] + y, ep);
+        if (wave == 0) {
+            const int r = t & 3;
+            const float y = ((red[r] + red[4 + r]) + (red[8 + r] + red[12 + r])) * sclD;
+            put_hidden4(rs, W_HO, b, hres[r] + y, ep, lane);
         }
         MDX_TRACE(16 * l + 7);
 
@@ -900,7 +917,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         const float4 nwE = reinterpret_cast<const float4*>(Ly.post_norm)[t];
         const float sclE = Ly.sgu ? Ly.sgu[rowE(t < 24 ? t : 0)] : 1.0f;
         {
-            int wd[2] = {W_HO + 8 * t, W_HO + 8 * t + 4};
+            const int wb = W_HO + (b % NREP) * (2 * D) + 8 * t;
+            int wd[2] = {wb, wb + 4};
             u32x4 v[2];
             const bool ok = ll_wait<2>(rs, wd, v, ep, dead);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
@@ -958,11 +976,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * l + 10);
         cm_dot<KIND, 4, FF>(wF, xs4, red, t);
         __syncthreads();
-        if (t < 4) {
-            const float y = ((red[t] + red[4 + t]) + (red[8 + t] + red[12 + t])) * sclF;
-            const float hn = hres[t] + y;
-            ll_put_f32(xb, W_HD + 2 * (4 * b + t), hn, ep);
-            if (last) a.hidden_out[4 * b + t] = hn;
+        if (wave == 0) {
+            const int r = t & 3;
+            const float y = ((red[r] + red[4 + r]) + (red[8 + r] + red[12 + r])) * sclF;
+            const float hn = hres[r] + y;
+            put_hidden4(rs, W_HD, b, hn, ep, lane);
+            if (last && t < 4) a.hidden_out[4 * b + t] = hn;
         }
         MDX_TRACE(16 * l + 11);
         __syncthreads();   // hres / red reuse
@@ -976,7 +995,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         float sc1 = 0.0f;
         const float4 nw = reinterpret_cast<const float4*>(a.final_norm)[t];
         {
-            int wd[2] = {W_HD + 8 * t, W_HD + 8 * t + 4};
+            const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
+            int wd[2] = {wb, wb + 4};
             u32x4 v[2];
             const bool ok = ll_wait<2>(rs, wd, v, ep_last, dead);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
