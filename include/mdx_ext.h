@@ -35,11 +35,17 @@ const char* mdx_last_error(void);
  * traffic: the calibration run for HBM byte counters). */
 int mdx_copy_probe(size_t bytes, int iters);
 
-/* Decode path of a context: 1 when a step is one cooperative launch of the
- * whole model (the 0.6B shape with one weight kind and the INT8 lm_head;
- * MDX_PERSIST=0 in the environment at creation turns it off), 0 when it is
- * the per-stage kernel sequence. */
+/* Decode path of a context: 1 when a step is one launch of the whole model
+ * (the 0.6B shape with one weight kind and the INT8 lm_head; MDX_PERSIST=0 in
+ * the environment at creation turns it off), 0 when it is the per-stage
+ * kernel sequence.  The launch is an ordinary one; if its waits time out
+ * (grid not co-resident) the step is run again as a cooperative launch, and
+ * the context keeps launching cooperatively. */
 int mdx_decode_path(const MatmulDecoderContext* ctx);
+/* Test hook: the next one-launch step polls each exchange at most `rounds`
+ * times before giving up (0: the default), which forces the timeout-and-retry
+ * path without any workgroup waiting long. */
+int mdx_debug_persist_spin_limit(MatmulDecoderContext* ctx, unsigned rounds);
 
 /* One decode step of the one-launch path with per-workgroup timestamps
  * (100 MHz device clock) at every stage boundary: out[256][E] with E

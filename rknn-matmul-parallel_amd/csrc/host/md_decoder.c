@@ -10,6 +10,7 @@
  * back the argmax (and the logits when the caller asks for them).
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -64,6 +65,8 @@ struct MatmulDecoderContext {
     int capture_M;
     int use_graphs;          /* 0 when MDX_GRAPHS=0: same kernels, launched one by one */
     int persist;             /* 1: decode steps run as one cooperative launch */
+    int persist_coop;        /* 1: launch it cooperatively (after an ordinary launch timed out) */
+    unsigned spin_once;      /* test hook: spin limit of the next one-launch step (0: default) */
     void* d_xbuf;            /* exchange words of the persistent step */
     mdx_persist_args pargs;
     mdx_state* h_state;
@@ -696,7 +699,27 @@ static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
     c->pargs.head = head;
     c->pargs.advance = 1;
     c->pargs.out_tokens = out_tokens;
+    c->pargs.cooperative = c->persist_coop;
+    c->pargs.spin_limit = c->spin_once;
+    c->spin_once = 0;
     return mdx_launch_persist_step(&c->pargs, c->stream);
+}
+
+/* One-launch steps of different contexts in this process never run at the
+ * same time: an ordinary launch relies on its grid being co-resident, which
+ * two concurrent grids of 256 CU-filling workgroups would not be.  (A grid of
+ * another process can still crowd one out; the step then times out and is
+ * retried as a cooperative launch, see persist_retry.) */
+static pthread_mutex_t g_persist_mu = PTHREAD_MUTEX_INITIALIZER;
+
+/* After a timed-out ordinary launch: switch the context to cooperative
+ * launches.  Returns 1 when the caller should run the step again (the state
+ * is uploaded again; the K/V rows the failed step wrote are rewritten). */
+static int persist_retry(MatmulDecoderContext* c) {
+    if (!c->persist || c->persist_coop) return 0;
+    c->persist_coop = 1;
+    fprintf(stderr, "[MatmulDecoder] one-launch step timed out; retrying with cooperative launches\n");
+    return 1;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -968,6 +991,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
          * either; use head 0 like step_head(…, 0, …) */
         return matmul_decoder_step_head(c, token_id, embedding, 0, output_logits);
     }
+    if (c->persist) pthread_mutex_lock(&g_persist_mu);
     rc = set_state(c, token_id, embedding);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
     if (c->persist) {
@@ -982,11 +1006,13 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     if (!rc && output_logits) rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    if (c->persist) pthread_mutex_unlock(&g_persist_mu);
     if (rc) {
         fprintf(stderr, "[MatmulDecoder] step failed: %s\n", mdxrt_last_error());
         return MATMUL_DECODER_ERR_RKNN;
     }
     if (c->h_state->pad[1]) {
+        if (persist_retry(c)) return do_step(c, token_id, embedding, output_logits, want_head);
         fprintf(stderr, "[MatmulDecoder] step failed: a workgroup timed out waiting for another\n");
         return MATMUL_DECODER_ERR_RKNN;
     }
@@ -1210,6 +1236,7 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
     }
     if (!c->persist && c->use_graphs && !c->g_greedy && capture(c, seq_greedy, &c->g_greedy))
         return MATMUL_DECODER_ERR_RKNN;
+    if (c->persist) pthread_mutex_lock(&g_persist_mu);
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
     c->h_state->token = first_token;
@@ -1220,9 +1247,11 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    if (c->persist) pthread_mutex_unlock(&g_persist_mu);
     if (!rc) rc = mdxrt_d2h(out_tokens, c->d_tokens, (size_t)n_steps * 4);
     if (rc) return MATMUL_DECODER_ERR_RKNN;
     if (c->h_state->pad[1]) {
+        if (persist_retry(c)) return mdx_generate_greedy(c, first_token, n_steps, out_tokens, device_ms);
         fprintf(stderr, "[MatmulDecoder] generate failed: a workgroup timed out waiting for another\n");
         return MATMUL_DECODER_ERR_RKNN;
     }
@@ -1325,6 +1354,7 @@ int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* ou
     if ((long long)cap < 256LL * ev) return MATMUL_DECODER_ERR_INVALID_ARG;
     unsigned long long* d = NULL;
     if (mdxrt_malloc((void**)&d, (size_t)256 * ev * 8)) return MATMUL_DECODER_ERR_MEMORY;
+    pthread_mutex_lock(&g_persist_mu);
     rc = set_state(c, token_id, NULL);
     if (!rc) rc = mdxrt_fill_u32(d, 0u, (size_t)256 * ev * 2, c->stream);
     c->pargs.trace = d;
@@ -1334,11 +1364,19 @@ int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* ou
     c->pargs.trace_stride = 0;
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    pthread_mutex_unlock(&g_persist_mu);
     if (!rc) rc = mdxrt_d2h(out, d, (size_t)256 * ev * 8);
     mdxrt_free(d);
     if (rc || c->h_state->pad[1]) return MATMUL_DECODER_ERR_RKNN;
     c->seq_len++;
     return ev;
+}
+
+int mdx_debug_persist_spin_limit(MatmulDecoderContext* c, unsigned rounds) {
+    if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
+    if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    c->spin_once = rounds;
+    return 0;
 }
 
 int mdx_decode_path(const MatmulDecoderContext* c) {

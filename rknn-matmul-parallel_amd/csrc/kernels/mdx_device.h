@@ -146,6 +146,10 @@ typedef struct {
     int n_layers, vocab, max_seq, rope_style;
     int head;              /* 1: final norm + INT8 lm_head + argmax; 0: layers only */
     int advance;           /* state->pos += advance at the end of the step */
+    int cooperative;       /* 1: hipLaunchCooperativeKernel (guaranteed co-residency);
+                              0: ordinary launch of the same grid (less launch latency;
+                              if the grid is not co-resident the waits time out and the
+                              step reports the failure in state->pad[1]) */
     float eps;
     mdx_state* state;
     mdx_persist_layer l0;              /* layer 0; layer l's pointers are l0's plus
@@ -166,6 +170,7 @@ typedef struct {
     int* out_tokens;                   /* optional greedy output list (state->n_out) */
     unsigned long long* trace;         /* optional [256][trace_stride] timestamps */
     int trace_stride;                  /* >= mdx_persist_trace_events(n_layers) */
+    unsigned spin_limit;               /* polling rounds before a wait gives up; 0: default */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */

@@ -48,7 +48,7 @@ constexpr int D = 1024, NQ = 16, NKV = 8, HD = 128, FF = 3072;
 constexpr int QD = NQ * HD, KVD = NKV * HD;
 constexpr int GRP = NB / NKV;           // workgroups per KV head
 constexpr int PP = 4;                   // 16-position K/V passes requested ahead
-constexpr unsigned kSpinLimit = 1u << 18;
+constexpr unsigned kSpinLimit = 1u << 18;   // polling rounds before a wait gives up
 
 // exchange buffer layout, in 32-bit words
 constexpr int W_CTRL = 0;                          // [0] step counter
@@ -88,6 +88,7 @@ struct PArgs {
     int* out_tokens;
     unsigned long long* trace;  // optional [NB][trace_stride] 100 MHz timestamps
     int trace_stride;
+    unsigned spin_limit;
 };
 
 // Timestamp of event ev for this workgroup (thread 0), when tracing is on.
@@ -151,10 +152,10 @@ __device__ __forceinline__ void put_hidden4(__amdgpu_buffer_rsrc_t rs, int base,
 }
 
 // Polls N 16-byte groups until every word carries epoch ep.  Returns false
-// after kSpinLimit rounds (the data is then stale; the caller stops waiting).
+// after `limit` rounds (the data is then stale; the caller stops waiting).
 template <int N>
 __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&word)[N],
-                                        u32x4 (&v)[N], unsigned ep, bool dead) {
+                                        u32x4 (&v)[N], unsigned ep, bool dead, unsigned limit) {
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = ll_load(rs, word[i]);
     if (dead) return true;
@@ -169,7 +170,7 @@ __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&w
             }
         }
         if (all) return true;
-        if (spin > kSpinLimit) return false;
+        if (spin > limit) return false;
     }
 }
 
@@ -179,16 +180,16 @@ __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&w
 // compete with the writes and with the other readers' polls).
 template <int N>
 __device__ __forceinline__ bool ll_wait_probe(__amdgpu_buffer_rsrc_t rs, const int (&word)[N],
-                                              u32x4 (&v)[N], unsigned ep, bool dead) {
+                                              u32x4 (&v)[N], unsigned ep, bool dead, unsigned limit) {
     int w0[1] = {word[0]};
     u32x4 v0[1];
-    bool ok = ll_wait<1>(rs, w0, v0, ep, dead);
+    bool ok = ll_wait<1>(rs, w0, v0, ep, dead, limit);
     v[0] = v0[0];
     int wr[N - 1];
     u32x4 vr[N - 1];
 #pragma unroll
     for (int i = 1; i < N; i++) wr[i - 1] = word[i];
-    ok = ll_wait<N - 1>(rs, wr, vr, ep, dead) && ok;
+    ok = ll_wait<N - 1>(rs, wr, vr, ep, dead, limit) && ok;
 #pragma unroll
     for (int i = 1; i < N; i++) v[i] = vr[i - 1];
     return ok;
@@ -530,6 +531,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     const int mode = a.st->mode;
     int tok = a.st->token;
     bool dead = false;
+    const unsigned spin_lim = a.spin_limit;
 
     // attention work split of this workgroup
     const int j = b % NKV, s = b / NKV;
@@ -604,7 +606,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
             u32x4 v[2];
-            const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead);
+            const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
             if (__syncthreads_or(!ok)) dead = true;
@@ -648,7 +650,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         {
             int wd[1] = {W_QKV + j * 1024 + 4 * t};
             u32x4 v[1];
-            const bool ok = ll_wait<1>(rs, wd, v, ep, dead);
+            const bool ok = ll_wait<1>(rs, wd, v, ep, dead, spin_lim);
             qkv_s[2 * t] = ll_f32(v[0].x, v[0].y);
             qkv_s[2 * t + 1] = ll_f32(v[0].z, v[0].w);
             if (__syncthreads_or(!ok)) dead = true;
@@ -845,7 +847,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0, base + 12 + 256 * hh + 2 * d0,
                          base + 16 + 256 * hh + 2 * d0, base + 20 + 256 * hh + 2 * d0};
             u32x4 v[5];
-            if (!ll_wait<5>(rs, wd, v, ep, dead)) dead = true;
+            if (!ll_wait<5>(rs, wd, v, ep, dead, spin_lim)) dead = true;
             const bool mine = lane < 32;
             const float m = mine ? ll_f32(v[0].x, v[0].y) : -INFINITY;
             const float M = half_max_dpp(m);
@@ -885,7 +887,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 const int wb = W_ATT + (b % NREP) * QD + 16 * u;
                 int wd[4] = {wb, wb + 4, wb + 8, wb + 12};
                 u32x4 v[4];
-                ok = ll_wait_probe<4>(rs, wd, v, ep, dead);
+                ok = ll_wait_probe<4>(rs, wd, v, ep, dead, spin_lim);
                 uint4 x0, x1;
                 x0.x = (v[0].x & 0xffffu) | (v[0].y << 16);
                 x0.y = (v[0].z & 0xffffu) | (v[0].w << 16);
@@ -920,7 +922,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int wb = W_HO + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
             u32x4 v[2];
-            const bool ok = ll_wait<2>(rs, wd, v, ep, dead);
+            const bool ok = ll_wait<2>(rs, wd, v, ep, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
             if (__syncthreads_or(!ok)) dead = true;
@@ -962,7 +964,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int wb = W_ACT + (b % NREP) * (NB * 16) + 16 * t;
             int wd[3] = {wb, wb + 4, wb + 8};
             u32x4 v[3];
-            const bool ok = ll_wait_probe<3>(rs, wd, v, ep, dead);
+            const bool ok = ll_wait_probe<3>(rs, wd, v, ep, dead, spin_lim);
             uint2* x2 = reinterpret_cast<uint2*>(xs4);
 #pragma unroll
             for (int k = 0; k < 3; k++) {
@@ -998,7 +1000,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
             u32x4 v[2];
-            const bool ok = ll_wait<2>(rs, wd, v, ep_last, dead);
+            const bool ok = ll_wait<2>(rs, wd, v, ep_last, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
             if (__syncthreads_or(!ok)) dead = true;
@@ -1069,7 +1071,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         {
             int wd[1] = {W_AMAX + 4 * t};
             u32x4 v[1];
-            const bool ok = ll_wait<1>(rs, wd, v, ep_head, dead);
+            const bool ok = ll_wait<1>(rs, wd, v, ep_head, dead, spin_lim);
             const unsigned hi = (v[0].x & 0xffffu) | (v[0].y << 16);
             const unsigned lo = (v[0].z & 0xffffu) | (v[0].w << 16);
             k = ((unsigned long long)hi << 32) | lo;
@@ -1177,15 +1179,18 @@ int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
     a.out_tokens = p->out_tokens;
     a.trace = p->trace;
     a.trace_stride = p->trace_stride;
+    a.spin_limit = p->spin_limit ? p->spin_limit : kSpinLimit;
     if (a.trace && a.trace_stride < 16 * a.n_layers + 4) return -1;
-    // MDX_COOP=0 issues the same grid as an ordinary launch (for tools that do
-    // not follow cooperative launches).  The grid still fits the device one
-    // workgroup per CU, and every wait is bounded, so a workgroup that did
-    // not become resident would end the step with an error, not a hang.
-    static const int coop = [] {
+    // MDX_COOP=1 / MDX_COOP=0 force the launch kind over the caller's choice
+    // (MDX_COOP=0 serves tools that do not follow cooperative launches).  The
+    // grid fits the device one workgroup per CU and every wait is bounded, so a
+    // workgroup that does not become resident ends the step with an error, not
+    // a hang.
+    static const int force = [] {
         const char* e = getenv("MDX_COOP");
-        return !(e && e[0] == '0');
+        return e && e[0] == '0' ? 0 : (e && e[0] == '1' ? 1 : -1);
     }();
+    const int coop = force >= 0 ? force : (p->cooperative ? 1 : 0);
     if (!coop) {
         hipLaunchKernelGGL(k, dim3(NB), dim3(NT), 0, (hipStream_t)stream, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;

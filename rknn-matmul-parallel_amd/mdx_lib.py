@@ -109,6 +109,7 @@ def lib() -> C.CDLL:
             "mdx_last_error": (C.c_char_p, []),
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
             "mdx_decode_path": (C.c_int, [P]),
+            "mdx_debug_persist_spin_limit": (C.c_int, [P, C.c_uint]),
             "mdx_trace_step": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint64), C.c_int]),
             "mdx_kv_fill_normal": (C.c_int, [P, C.c_int, C.c_uint64]),
             "mdx_kv_read": (C.c_int, [P, C.c_int, C.c_int, C.c_int, _F, _F]),
@@ -296,8 +297,12 @@ class Decoder:
 
     @property
     def path(self) -> int:
-        """1: one cooperative launch per step; 0: per-stage kernels."""
+        """1: one launch per step; 0: per-stage kernels."""
         return lib().mdx_decode_path(self.h)
+
+    def force_spin_limit(self, rounds: int):
+        """Next one-launch step gives up a wait after `rounds` polls (test hook)."""
+        _check(lib().mdx_debug_persist_spin_limit(self.h, rounds), "spin_limit")
 
     def close(self):
         if self.h:

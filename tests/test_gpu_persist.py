@@ -131,3 +131,28 @@ def test_greedy_tokens_match_oracle(mdx, gpu, oracle_lib, models, quant):
     print(f"q{quant}: gpu {toks_g}\n    oracle {toks_o}\n    min margin {min(margins):.3g}")
     assert list(toks_g) == list(toks_o)
     assert g.seq_len == 316
+
+
+def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models, capfd):
+    """A one-launch step whose waits give up (forced here with a 1-round spin
+    limit, as a grid that is not co-resident would) reports the timeout in the
+    state; the host runs the step again as a cooperative launch, and the
+    result equals an undisturbed context's."""
+    cfg, get = models
+    path = get(1)
+    g_ref, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    g, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    for d in (g_ref, g):
+        d.kv_fill_normal(200, 13)
+    t_ref, l_ref = g_ref.step(321)
+    g.force_spin_limit(1)
+    t, lg = g.step(321)
+    err = capfd.readouterr().err
+    print(err)
+    assert "retrying with cooperative launches" in err
+    assert t == t_ref and np.array_equal(lg, l_ref)
+    assert g.seq_len == g_ref.seq_len == 201
+    for tok in (7, 4000):   # later steps (cooperative now) still agree
+        t_ref, l_ref = g_ref.step(tok)
+        t, lg = g.step(tok)
+        assert t == t_ref and np.array_equal(lg, l_ref)
