@@ -993,9 +993,13 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     const unsigned ep_head = step_epoch(E, L, L);
     if (a.head) {
         // ================= lm_head (INT8 rows, fp16 activations) + argmax ==========
-        uint4 w1[U];
-        float sc1 = 0.0f;
+        // three row batches per wave: two in flight while one is multiplied
+        uint4 w1[U], w2[U];
+        float sc1 = 0.0f, sc2 = 0.0f;
         const float4 nw = reinterpret_cast<const float4*>(a.final_norm)[t];
+        // the second batch is requested before the wait (measured: the longer
+        // wait costs less than the later start of the stream)
+        if (rb + wave * U + 4 * U < re) load_rows(w1, sc1, rb + wave * U + 4 * U);
         {
             const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
@@ -1030,14 +1034,16 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 }
             }
         };
-        for (int base = rb + wave * U; base < re; base += 8 * U) {
-            const int nb1 = base + 4 * U;
-            if (nb1 < re) load_rows(w1, sc1, nb1);
+        // this wave's batches start at rb + wave*U, 4U rows apart
+        for (int base = rb + wave * U; base < re; base += 12 * U) {
+            if (base + 8 * U < re) load_rows(w2, sc2, base + 8 * U);
             consume(w0, sc0, base);
-            if (nb1 >= re) break;
-            const int nb2 = nb1 + 4 * U;
-            if (nb2 < re) load_rows(w0, sc0, nb2);
-            consume(w1, sc1, nb1);
+            if (base + 4 * U >= re) break;
+            if (base + 12 * U < re) load_rows(w0, sc0, base + 12 * U);
+            consume(w1, sc1, base + 4 * U);
+            if (base + 8 * U >= re) break;
+            if (base + 16 * U < re) load_rows(w1, sc1, base + 16 * U);
+            consume(w2, sc2, base + 8 * U);
         }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
