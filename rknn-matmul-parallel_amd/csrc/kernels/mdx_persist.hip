@@ -428,11 +428,11 @@ __device__ __forceinline__ void cm_dot(const uint4 (&w)[NWT], const uint4* xs4, 
 
 // ---- small helpers ----------------------------------------------------------
 
-__device__ __forceinline__ float block_sum4(float v, float* ws, int t) {
-    v = wave_sum_dpp(v);
+// Publishes this wave's sum of h^2 to ws[wave]; the barrier that follows
+// (the wait's __syncthreads_or) makes the four partials visible.
+__device__ __forceinline__ void wave_ss(const float (&h)[4], float* ws, int t) {
+    const float v = wave_sum_dpp(h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3]);
     if ((t & 63) == 0) ws[t >> 6] = v;
-    __syncthreads();
-    return (ws[0] + ws[1]) + (ws[2] + ws[3]);
 }
 
 // fp16 x[4t..4t+4) = fp16((h * rms) * w) into the LDS activation vector.
@@ -510,7 +510,6 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     __shared__ float red[64];
     __shared__ float ws[8];
     __shared__ float hres[4];
-    __shared__ float gu_s[24];
     __shared__ float qkv_s[512];
     __shared__ float q_s[2 * HD];
     __shared__ float kn_s[HD];
@@ -609,7 +608,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const bool ok = ll_wait<2>(rs, wd, v, ep_prev, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            wave_ss(h, ws, t);
             if (__syncthreads_or(!ok)) dead = true;
+        } else {
+            wave_ss(h, ws, t);
+            __syncthreads();
         }
         // weight requests go out after the wait, so they do not queue in front
         // of the exchange's own reads
@@ -629,8 +632,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * l + 1);
         if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
         {
-            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
-            const float tot = block_sum4(ss, ws, t);
+            const float tot = (ws[0] + ws[1]) + (ws[2] + ws[3]);
             const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
             norm_to_x(h, nwA, rms, xs4, t);
         }
@@ -925,35 +927,42 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const bool ok = ll_wait<2>(rs, wd, v, ep, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            wave_ss(h, ws + 4, t);
             if (__syncthreads_or(!ok)) dead = true;
         }
         MDX_TRACE(16 * l + 8);
         if (t == b) { hres[0] = h[0]; hres[1] = h[1]; hres[2] = h[2]; hres[3] = h[3]; }
         {
-            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
-            const float tot = block_sum4(ss, ws + 4, t);
+            const float tot = (ws[4] + ws[5]) + (ws[6] + ws[7]);
             const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
             norm_to_x(h, nwE, rms, xs4, t);
         }
         __syncthreads();
         rm_dot<KIND, 24, D>(wE, xs4, red, t);
         __syncthreads();
-        if (t < 24) {
-            float y = red[t * SE::NSPLIT];
-            if (SE::NSPLIT == 2) y = y + red[t * SE::NSPLIT + 1];
-            gu_s[t] = y * sclE;
-        }
-        __syncthreads();
-        if (t < 3 * NREP) {
-            // lane t: copy t / 3, values 4 (t % 3) .. +3 in one 16-byte store
-            const int c = t % 3;
-            const unsigned e = ep << 16;
-            u32x4 pk;
-            pk.x = f32_to_f16_bits(silu_mul(gu_s[4 * c + 0], gu_s[12 + 4 * c + 0])) | e;
-            pk.y = f32_to_f16_bits(silu_mul(gu_s[4 * c + 1], gu_s[12 + 4 * c + 1])) | e;
-            pk.z = f32_to_f16_bits(silu_mul(gu_s[4 * c + 2], gu_s[12 + 4 * c + 2])) | e;
-            pk.w = f32_to_f16_bits(silu_mul(gu_s[4 * c + 3], gu_s[12 + 4 * c + 3])) | e;
-            ll_put4(rs, W_ACT + (t / 3) * (NB * 16) + 16 * b + 4 * c, pk);
+        if (wave == 0) {
+            // lane k < 24: row k (gate k < 12, up k - 12); lane k < 12 then
+            // holds feature k's activation, broadcast with readlane
+            const int r = lane < 24 ? lane : 0;
+            float y = red[r * SE::NSPLIT];
+            if (SE::NSPLIT == 2) y = y + red[r * SE::NSPLIT + 1];
+            y = y * sclE;
+            const float u = __shfl(y, (lane + 12) & 63, 64);
+            const unsigned act = f32_to_f16_bits(silu_mul(y, u));
+            unsigned av[12];
+#pragma unroll
+            for (int k = 0; k < 12; k++) av[k] = __builtin_amdgcn_readlane(act, k);
+            if (lane < 3 * NREP) {
+                // lane: copy lane / 3, features 4 (lane % 3) .. +3 in one 16-byte store
+                const int c = lane % 3;
+                const unsigned e = ep << 16;
+                u32x4 pk;
+                pk.x = (c == 0 ? av[0] : c == 1 ? av[4] : av[8]) | e;
+                pk.y = (c == 0 ? av[1] : c == 1 ? av[5] : av[9]) | e;
+                pk.z = (c == 0 ? av[2] : c == 1 ? av[6] : av[10]) | e;
+                pk.w = (c == 0 ? av[3] : c == 1 ? av[7] : av[11]) | e;
+                ll_put4(rs, W_ACT + (lane / 3) * (NB * 16) + 16 * b + 4 * c, pk);
+            }
         }
         MDX_TRACE(16 * l + 9);
 
@@ -1007,12 +1016,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const bool ok = ll_wait<2>(rs, wd, v, ep_last, dead, spin_lim);
             h[0] = ll_f32(v[0].x, v[0].y); h[1] = ll_f32(v[0].z, v[0].w);
             h[2] = ll_f32(v[1].x, v[1].y); h[3] = ll_f32(v[1].z, v[1].w);
+            wave_ss(h, ws, t);
             if (__syncthreads_or(!ok)) dead = true;
         }
         MDX_TRACE(16 * L + 0);
         {
-            const float ss = h[0] * h[0] + h[1] * h[1] + h[2] * h[2] + h[3] * h[3];
-            const float tot = block_sum4(ss, ws, t);
+            const float tot = (ws[0] + ws[1]) + (ws[2] + ws[3]);
             const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
             norm_to_x(h, nw, rms, xs4, t);
         }
