@@ -231,7 +231,7 @@ def main() -> int:
                    "hidden": 1024, "heads": "16q/8kv x128", "ffn": 3072, "vocab": 151936,
                    "kv_start": KV_PREFILL, "start_token": START_TOKEN},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_persist_step<f16> (one cooperative launch per token: 28 layers + "
+                     "kernel": "k_persist_step<f16> (one launch per token: 28 layers + "
                                "INT8 lm_head + argmax)" if path_kind == 1 else
                                "per-stage kernel sequence (one-launch step unavailable)",
                      "achieved": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
