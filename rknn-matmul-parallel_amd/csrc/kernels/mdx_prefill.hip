@@ -187,6 +187,22 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
     const uint16_t* const arow[4] = {x16 + (size_t)min(c16, M - 1) * K, x16 + (size_t)min(16 + c16, M - 1) * K,
                                      x16 + (size_t)min(32 + c16, M - 1) * K, x16 + (size_t)min(48 + c16, M - 1) * K};
 
+    // The epilogue's outputs of this thread all lie in column tid % kNT (2048
+    // outputs, 256 threads): its scales are requested now, not after the sums.
+    float sc_a = 1.0f, sc_b = 1.0f;
+    if (!part && scale) {
+        const int col = tid % kNT;
+        if (swiglu) {
+            const int f = tile * (kNT / 2) + col;
+            if (col < kNT / 2 && f < N / 2) {
+                sc_a = scale[f];
+                sc_b = scale[N / 2 + f];
+            }
+        } else if (tile * kNT + col < N) {
+            sc_a = scale[tile * kNT + col];
+        }
+    }
+
     float4_t acc[2][4];
 #pragma unroll
     for (int t = 0; t < 2; t++)
@@ -234,7 +250,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
             float u = red[0][row * kNT + col + kNT / 2];
 #pragma unroll
             for (int wv = 1; wv < kGemmWaves; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
-            const float gs = v * (scale ? scale[f] : 1.0f), us = u * (scale ? scale[cols + f] : 1.0f);
+            const float gs = v * sc_a, us = u * sc_b;
             float act;
             if (f < (cols & ~3)) act = silu_mul(gs, us);
             else act = (gs / (1.0f + expf(-gs))) * us;     // reference tail formula
@@ -242,7 +258,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
         } else {
             const int n = tile * kNT + col;
             if (n >= N) continue;
-            const float y = v * (scale ? scale[n] : 1.0f);
+            const float y = v * sc_a;
             if (epi == 1) out_f32[(size_t)row * N + n] = out_f32[(size_t)row * N + n] + y;
             else out_f32[(size_t)row * N + n] = y;
         }
