@@ -156,3 +156,36 @@ def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models,
         t_ref, l_ref = g_ref.step(tok)
         t, lg = g.step(tok)
         assert t == t_ref and np.array_equal(lg, l_ref)
+
+
+def test_two_contexts_in_two_threads(mdx, gpu, oracle_lib, models, capfd):
+    """Two contexts stepping at the same time from two threads: their one-launch
+    steps are serialised inside the library, so neither grid is crowded out
+    (no timeout, no cooperative retry) and each produces what it produces alone."""
+    import threading
+    cfg, get = models
+    path = get(2)
+    ref = []
+    for seed in (3, 4):
+        g, _ = _pair(mdx, oracle_lib, cfg, path, 2)
+        g.kv_fill_normal(100, seed)
+        ref.append(g.generate_greedy(11, 24)[0])
+        g.close()
+    ctx = []
+    for seed in (3, 4):
+        g, _ = _pair(mdx, oracle_lib, cfg, path, 2)
+        g.kv_fill_normal(100, seed)
+        ctx.append(g)
+    out = [None, None]
+
+    def run(i):
+        out[i] = ctx[i].generate_greedy(11, 24)[0]
+
+    th = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for x in th:
+        x.start()
+    for x in th:
+        x.join(timeout=120)
+    err = capfd.readouterr().err
+    assert "retrying with cooperative launches" not in err
+    assert out[0] == ref[0] and out[1] == ref[1]
