@@ -315,6 +315,131 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     }
 }
 
+// INT8 lm_head with K = 1024 (one 16-byte chunk per lane is a whole row):
+// block b streams rows [b*N/grid, (b+1)*N/grid); each wave takes batches of
+// 16 rows, 4 batches apart, with three batches in registers (two in flight
+// while one is multiplied).  x = fp16(RMSNorm(hidden)).  Each block stores its
+// argmax key; arrival is counted in 8 group counters (so no single address
+// takes all the atomics) and the last block reduces the keys and does the
+// step bookkeeping of k_gemv's EP_LOGITS.
+constexpr int kLmRows = 16;
+constexpr int kLmBlocks = 256;
+constexpr int kLmGroups = 8;
+__global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
+    constexpr int U = kLmRows;
+    constexpr int PER = 64 / U;
+    __shared__ uint4 xs[128];
+    __shared__ float red[4];
+    __shared__ unsigned long long bkey[4];
+    __shared__ int last_block;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rb = (int)(((long long)blockIdx.x * a.N) / gridDim.x);
+    const int re = (int)(((long long)(blockIdx.x + 1) * a.N) / gridDim.x);
+    auto load = [&](uint4 (&w)[U], float& sc, int base) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int r = min(base + u, re - 1);
+            w[u] = *reinterpret_cast<const uint4*>(a.w + (size_t)r * 1024 + lane * 16);
+        }
+        sc = a.scale ? a.scale[min(base + lane / PER, re - 1)] : 1.0f;
+    };
+    uint4 w0[U], w1[U], w2[U];
+    float sc0 = 0.0f, sc1 = 0.0f, sc2 = 0.0f;
+    const int first = rb + wave * U;
+    if (first < re) load(w0, sc0, first);
+    if (first + 4 * U < re) load(w1, sc1, first + 4 * U);
+    build_x<false>(a, xs, red);
+    __syncthreads();
+    const uint4 x0 = xs[2 * lane], x1 = xs[2 * lane + 1];
+    unsigned long long best = 0ull;
+    auto consume = [&](const uint4 (&w)[U], float sc, int base) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = dot16_i8(w[u], x0, x1, 0.0f);
+        const float tot = reduce_scatter<U, 64>(v, lane);
+        const int r = base + lane / PER;
+        if ((lane % PER) == 0 && r < re) {
+            const float y = tot * sc;
+            a.out_f32[r] = y;
+            if (y == y) {
+                const unsigned long long k = argmax_key(y, r);
+                best = k > best ? k : best;
+            }
+        }
+    };
+    for (int base = first; base < re; base += 12 * U) {
+        if (base + 8 * U < re) load(w2, sc2, base + 8 * U);
+        consume(w0, sc0, base);
+        if (base + 4 * U >= re) break;
+        if (base + 12 * U < re) load(w0, sc0, base + 12 * U);
+        consume(w1, sc1, base + 4 * U);
+        if (base + 8 * U >= re) break;
+        if (base + 16 * U < re) load(w1, sc1, base + 16 * U);
+        consume(w2, sc2, base + 8 * U);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned lo = __shfl_xor((unsigned)(best & 0xffffffffull), off, 64);
+        const unsigned hi = __shfl_xor((unsigned)(best >> 32), off, 64);
+        const unsigned long long k = ((unsigned long long)hi << 32) | lo;
+        best = k > best ? k : best;
+    }
+    if (lane == 0) bkey[wave] = best;
+    __syncthreads();
+    // scratch: [16, 48) group counters, [48, 52) group-done counter, [64, ...) keys
+    unsigned* cnt = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(a.amax_key) + 16);
+    unsigned* top = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(a.amax_key) + 48);
+    unsigned long long* keys = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(a.amax_key) + 64);
+    if (tid == 0) {
+        unsigned long long bk = bkey[0];
+        for (int w = 1; w < 4; w++) bk = bkey[w] > bk ? bkey[w] : bk;
+        keys[blockIdx.x] = bk;
+        __threadfence();
+        const int grp = blockIdx.x % kLmGroups;
+        const unsigned in_grp = (gridDim.x - grp + kLmGroups - 1) / kLmGroups;
+        int last = 0;
+        if (atomicAdd(&cnt[grp], 1u) == in_grp - 1) {
+            __threadfence();
+            last = atomicAdd(top, 1u) == kLmGroups - 1;
+        }
+        last_block = last;
+    }
+    __syncthreads();
+    if (last_block) {
+        __threadfence();
+        unsigned long long k = 0ull;
+        for (int i = tid; i < (int)gridDim.x; i += 256) {
+            const unsigned long long v = __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            k = v > k ? v : k;
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const unsigned lo = __shfl_xor((unsigned)(k & 0xffffffffull), off, 64);
+            const unsigned hi = __shfl_xor((unsigned)(k >> 32), off, 64);
+            const unsigned long long k2 = ((unsigned long long)hi << 32) | lo;
+            k = k2 > k ? k2 : k;
+        }
+        if (lane == 0) bkey[wave] = k;
+        __syncthreads();
+        if (tid < kLmGroups) cnt[tid] = 0u;
+    }
+    if (last_block && tid == 0) {
+        unsigned long long k = bkey[0];
+        for (int w = 1; w < 4; w++) k = bkey[w] > k ? bkey[w] : k;
+        *top = 0u;
+        const int tok = k ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+        mdx_state* st = a.st;
+        st->argmax = tok;
+        st->token = tok;
+        st->mode = 0;
+        if (a.out_tokens) {
+            a.out_tokens[st->n_out] = tok;
+            st->n_out = st->n_out + 1;
+        }
+        st->pos = st->pos + a.advance;
+    }
+}
+
 typedef void (*GemvKernel)(GemvArgs);
 
 template <int KIND>
@@ -773,7 +898,7 @@ int mdx_launch_gemv(const float* x, const mdx_wdesc* w, int x_fp32_exact, float*
     return launch_gemv(kind, a, rows_per_wave_for(a.N), 0, stream);
 }
 
-size_t mdx_lmhead_scratch_bytes(void) { return 16; }
+size_t mdx_lmhead_scratch_bytes(void) { return 64 + 8 * kLmBlocks; }
 
 int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const mdx_wdesc* w,
                       float* logits, void* scratch, mdx_state* state, int* out_tokens, int advance,
@@ -792,6 +917,10 @@ int mdx_launch_lmhead(const float* hidden, const float* norm_w, float eps, const
     a.advance = advance;
     // fp16 rows take fp32 activations here (the reference's CPU lm_head)
     const int kind = kind_from(w, 1);
+    if (kind == KI8 && w->K == 1024 && w->N >= kLmBlocks * kLmRows) {
+        hipLaunchKernelGGL(k_lmhead_i8_1k, dim3(kLmBlocks), dim3(256), 0, (hipStream_t)stream, a);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     return launch_gemv(kind, a, rows_per_wave_for(w->N), 1024, stream);
 }
 

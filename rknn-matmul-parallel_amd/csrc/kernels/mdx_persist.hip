@@ -273,89 +273,6 @@ struct ChunkMajor {
     static constexpr bool RAGGED = CPR % STEP != 0;
 };
 
-// The value of the partner lane at distance O (a symmetric pairing that
-// flips lane bit log2(O) and keeps the higher bits): DPP within a 16-lane
-// row, the gfx950 row swaps across rows.
-template <int O>
-__device__ __forceinline__ float partner(float v) {
-    if constexpr (O == 1) return dpp<0xB1>(v);        // quad_perm [1,0,3,2]
-    else if constexpr (O == 2) return dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-    else if constexpr (O == 4) return dpp<0x141>(v);  // row_half_mirror: i <-> 7-i
-    else return dpp<0x128>(v);                        // row_ror:8 (i <-> i^8)
-}
-
-// One butterfly step at distance O over nv live values: the lane with bit O
-// clear keeps the low half, its partner the high half; each adds the other's
-// copy of the half it keeps.
-template <int O, int NV>
-__device__ __forceinline__ void rs_step(float (&v)[NV], int nv, int lane) {
-    const int half = nv / 2;
-    if constexpr (O >= 16) {
-        // row swaps: (lo, hi) -> (own lo, partner lo) below, (partner hi, own hi) above
-#pragma unroll
-        for (int k = 0; k < NV / 2; k++) {
-            if (k < half) {
-                if constexpr (O == 32) {
-                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]),
-                                                                    __float_as_uint(v[k + half]), false, false);
-                    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-                } else {
-                    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]),
-                                                                    __float_as_uint(v[k + half]), false, false);
-                    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-                }
-            }
-        }
-    } else {
-        // bitwise select: keeps both reads static (a select of two array
-        // elements would otherwise become a dynamically indexed read)
-        const unsigned up = (lane & O) ? 0xffffffffu : 0u;
-#pragma unroll
-        for (int k = 0; k < NV / 2; k++) {
-            if (k < half) {
-                const unsigned lo = __float_as_uint(v[k]), hi = __float_as_uint(v[k + half]);
-                const float send = __uint_as_float((lo & up) | (hi & ~up));
-                const float keep = __uint_as_float((hi & up) | (lo & ~up));
-                v[k] = keep + partner<O>(send);
-            }
-        }
-    }
-}
-template <int O>
-__device__ __forceinline__ float sum_step(float v) {
-    if constexpr (O == 32) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    } else if constexpr (O == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    } else {
-        return v + partner<O>(v);
-    }
-}
-
-// Reduce-scatter of NV per-lane values over aligned groups of G lanes: on
-// return lane l holds the group total of value (l % G) / (G / NV).
-constexpr int ilog2(int x) { return x <= 1 ? 0 : 1 + ilog2(x / 2); }
-
-template <int NV, int G, int O = G / 2>
-__device__ __forceinline__ float reduce_scatter_from(float (&v)[NV], int nv, int lane) {
-    if constexpr (O == 0) {
-        return v[0];
-    } else {
-        if (nv > 1) {
-            rs_step<O, NV>(v, nv, lane);
-            return reduce_scatter_from<NV, G, O / 2>(v, nv / 2, lane);
-        }
-        v[0] = sum_step<O>(v[0]);
-        return reduce_scatter_from<NV, G, O / 2>(v, 1, lane);
-    }
-}
-template <int NV, int G>
-__device__ __forceinline__ float reduce_scatter(float (&v)[NV], int lane) {
-    return reduce_scatter_from<NV, G>(v, NV, lane);
-}
-
 // Row-major dot + reduction; red[r * NSPLIT + part] receives the row sums.
 template <int KIND, int R, int K, int NWT>
 __device__ __forceinline__ void rm_dot(const uint4 (&w)[NWT], const uint4* xs4, float* red, int t) {

@@ -215,15 +215,18 @@ def test_lm_head_int8_argmax(mdx, gpu, oracle_lib, V):
         assert tok == int(np.argmax(ref))
 
 
-def test_lm_head_argmax_ties_pick_lowest_index(mdx, gpu):
-    K, V = 64, 4096
+@pytest.mark.parametrize("K,V,ties", [(64, 4096, [10, 700, 3000]),
+                                      # the streaming K=1024 kernel: ties within one
+                                      # block's rows and across blocks
+                                      (1024, 16384, [4100, 4101, 9000, 16383])])
+def test_lm_head_argmax_ties_pick_lowest_index(mdx, gpu, K, V, ties):
     q = np.zeros((V, K), np.int8)
-    q[[10, 700, 3000], 0] = 5                       # three equal maxima
+    q[ties, 0] = 5                                  # equal maxima
     s = np.ones(V, np.float32)
     h = np.zeros(K, np.float32)
     h[0] = 1.0
     tok, lg = mdx.lmhead(1, K, V, q, s, h, np.ones(K, np.float32), 1e-6)
-    assert tok == 10 and lg[10] == lg[700] == lg[3000]
+    assert tok == ties[0] and all(lg[i] == lg[ties[0]] for i in ties)
 
 
 def test_lm_head_fp32_and_fp16_rows(mdx, gpu, oracle_lib):
