@@ -35,12 +35,16 @@ const char* mdx_last_error(void);
  * traffic: the calibration run for HBM byte counters). */
 int mdx_copy_probe(size_t bytes, int iters);
 
-/* Decode path of a context: 1 when a step is one launch of the whole model
- * (the 0.6B shape with one weight kind and the INT8 lm_head; MDX_PERSIST=0 in
- * the environment at creation turns it off), 0 when it is the per-stage
- * kernel sequence.  The launch is an ordinary one; if its waits time out
- * (grid not co-resident) the step is run again as a cooperative launch, and
- * the context keeps launching cooperatively. */
+/* Decode path of a context:
+ *   1  a step is one launch of the whole model (the 0.6B layer shape with one
+ *      weight kind and the single INT8 lm_head);
+ *   2  the layers are one launch and the lm_head a per-stage kernel after it
+ *      (the same layer shape with several lm_heads or the fp16 lm_head);
+ *   0  the per-stage kernel sequence.
+ * MDX_PERSIST=0 in the environment at creation selects 0.  The launch is an
+ * ordinary one; if its waits time out (grid not co-resident) the step is run
+ * again as a cooperative launch, and the context keeps launching
+ * cooperatively. */
 int mdx_decode_path(const MatmulDecoderContext* ctx);
 /* Test hook: the next one-launch step polls each exchange at most `rounds`
  * times before giving up (0: the default), which forces the timeout-and-retry
@@ -51,7 +55,7 @@ int mdx_debug_persist_spin_limit(MatmulDecoderContext* ctx, unsigned rounds);
  * (100 MHz device clock) at every stage boundary: out[256][E] with E
  * events per workgroup: 16 per layer, 3 for the lm_head, then the
  * workgroup's XCD index.  Returns E, or
- * MATMUL_DECODER_ERR_UNSUPPORTED when the context uses per-stage kernels. */
+ * MATMUL_DECODER_ERR_UNSUPPORTED unless the decode path is 1. */
 int mdx_trace_step(MatmulDecoderContext* ctx, int token_id, unsigned long long* out, int cap);
 
 /* matmul_decoder_step with the lm_head and argmax but without copying the

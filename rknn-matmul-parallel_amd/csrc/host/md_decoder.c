@@ -64,7 +64,8 @@ struct MatmulDecoderContext {
     int pgraph_next;
     int capture_M;
     int use_graphs;          /* 0 when MDX_GRAPHS=0: same kernels, launched one by one */
-    int persist;             /* 1: decode steps run as one cooperative launch */
+    int persist;             /* 1: the layers of a decode step run as one launch */
+    int persist_head;        /* 1: that launch also runs the INT8 lm_head and the argmax */
     int persist_coop;        /* 1: launch it cooperatively (after an ordinary launch timed out) */
     unsigned spin_once;      /* test hook: spin limit of the next one-launch step (0: default) */
     void* d_xbuf;            /* exchange words of the persistent step */
@@ -626,15 +627,18 @@ static int at_stride(const void* p0, const void* pl, int l, long long stride) {
     return (const char*)pl - (const char*)p0 == (long long)l * stride;
 }
 
-/* The whole step becomes one cooperative launch when the model has the shape
- * that kernel is built for, one weight kind throughout, the INT8 lm_head,
- * and layers laid out at a constant stride in the arena (always true for the
- * arena layout, checked anyway).  MDX_PERSIST=0 keeps the per-kernel path. */
+/* The layers of a step become one launch when the model has the shape that
+ * kernel is built for, one weight kind throughout, and layers laid out at a
+ * constant stride in the arena (always true for the arena layout, checked
+ * anyway).  With the single INT8 lm_head the same launch also runs the head
+ * and the argmax; multi-head models and the fp16 lm_head run their head as a
+ * per-stage kernel after it.  MDX_PERSIST=0 keeps the per-kernel path. */
 static void setup_persist(MatmulDecoderContext* c) {
     c->persist = 0;
+    c->persist_head = 0;
     const char* e = getenv("MDX_PERSIST");
     if (e && e[0] == '0') return;
-    if (c->n_lm > 1 || c->config.disable_npu_lm_head || c->L < 1 || c->V < 256) return;
+    if (c->L < 1) return;
     if (!mdx_persist_shape_ok(c->d, c->nq, c->nkv, c->hd, c->F)) return;
     const md_layer* l0 = &c->layers[0];
     const int kind = l0->qkv.kind;
@@ -687,8 +691,11 @@ static void setup_persist(MatmulDecoderContext* c) {
     a->cos_t = c->d_cos;
     a->sin_t = c->d_sin;
     a->final_norm = c->d_final_norm;
-    a->lm_w = (const int8_t*)c->lm.w;
-    a->lm_scale = c->lm.scale;
+    if (c->n_lm <= 1 && !c->config.disable_npu_lm_head && c->V >= 256 && c->lm.kind == MDX_W_I8) {
+        a->lm_w = (const int8_t*)c->lm.w;
+        a->lm_scale = c->lm.scale;
+        c->persist_head = 1;
+    }
     a->logits = c->d_logits;
     a->hidden_out = c->d_hidden;
     a->xbuf = c->d_xbuf;
@@ -696,6 +703,7 @@ static void setup_persist(MatmulDecoderContext* c) {
 }
 
 static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
+    if (head && !c->persist_head) return MATMUL_DECODER_ERR_INVALID_ARG;
     c->pargs.head = head;
     c->pargs.advance = 1;
     c->pargs.out_tokens = out_tokens;
@@ -860,7 +868,8 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     setup_persist(c);
     if (md_verbose())
         printf("[MatmulDecoder] decode step: %s\n",
-               c->persist ? "one cooperative launch" : "per-stage kernels");
+               c->persist ? (c->persist_head ? "one launch" : "layers in one launch, per-stage lm_head")
+                          : "per-stage kernels");
     return c;
 fail:
     fprintf(stderr, "[MatmulDecoder] create failed%s%s\n", mdxrt_last_error()[0] ? ": " : "",
@@ -994,9 +1003,15 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     if (c->persist) pthread_mutex_lock(&g_persist_mu);
     rc = set_state(c, token_id, embedding);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    if (c->persist) {
+    if (c->persist && (c->persist_head || !want_head)) {
         if (!rc) rc = launch_persist(c, want_head, NULL);
         if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
+    } else if (c->persist) {
+        /* the fp16 lm_head: layers in one launch (which advances the
+         * position), then the per-stage head */
+        if (!rc) rc = launch_persist(c, 0, NULL);
+        if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
+        if (!rc) rc = run_head(c, &c->lm, NULL, 0, c->stream);
     } else {
         if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
         if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
@@ -1028,7 +1043,8 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     c->stats.matmul_ms = layers_ms;
     c->stats.rebind_ms = 0.0f;
     c->stats.cpu_ops_ms = 0.0f;
-    c->stats.lm_head_ms = want_head ? head_ms : 0.0f;   /* 0 for the one-launch step (inside matmul_ms) */
+    /* 0 when the head runs inside the one launch (then it is in matmul_ms) */
+    c->stats.lm_head_ms = want_head ? head_ms : 0.0f;
     c->stats.convert_ms = total - layers_ms - (want_head ? head_ms : 0.0f);
     if (c->stats.convert_ms < 0) c->stats.convert_ms = 0;
     c->stats.n_steps++;
@@ -1058,14 +1074,27 @@ int matmul_decoder_step_head(MatmulDecoderContext* c, int token_id, const float*
     int rc = step_checks(c, token_id, embedding);
     if (rc) return rc;
     if (ensure_graphs(c)) return MATMUL_DECODER_ERR_RKNN;
+    if (c->persist) pthread_mutex_lock(&g_persist_mu);
     rc = set_state(c, token_id, embedding);
-    if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
-    if (!rc) rc = run_head(c, &c->lm_heads[lm_head_idx], NULL, 1, c->stream);
+    if (c->persist) {
+        /* the one launch advances the position; the head does not */
+        if (!rc) rc = launch_persist(c, 0, NULL);
+        if (!rc) rc = run_head(c, &c->lm_heads[lm_head_idx], NULL, 0, c->stream);
+    } else {
+        if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
+        if (!rc) rc = run_head(c, &c->lm_heads[lm_head_idx], NULL, 1, c->stream);
+    }
     if (!rc && output_logits)
         rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->lm_vocab * 4, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    if (c->persist) pthread_mutex_unlock(&g_persist_mu);
     if (rc) return MATMUL_DECODER_ERR_RKNN;
+    if (c->h_state->pad[1]) {
+        if (persist_retry(c)) return matmul_decoder_step_head(c, token_id, embedding, lm_head_idx, output_logits);
+        fprintf(stderr, "[MatmulDecoder] step failed: a workgroup timed out waiting for another\n");
+        return MATMUL_DECODER_ERR_RKNN;
+    }
     c->seq_len++;
     if (output_logits) memcpy(output_logits, c->h_io, (size_t)c->lm_vocab * 4);
     return c->h_state->argmax;
@@ -1242,8 +1271,16 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
     c->h_state->token = first_token;
     int rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
-    for (int i = 0; i < n_steps && !rc; i++)
-        rc = c->persist ? launch_persist(c, 1, c->d_tokens) : launch_seq(c, c->g_greedy, seq_greedy);
+    for (int i = 0; i < n_steps && !rc; i++) {
+        if (!c->persist) {
+            rc = launch_seq(c, c->g_greedy, seq_greedy);
+        } else if (c->persist_head) {
+            rc = launch_persist(c, 1, c->d_tokens);
+        } else {
+            rc = launch_persist(c, 0, NULL);
+            if (!rc) rc = run_head(c, &c->lm, c->d_tokens, 0, c->stream);
+        }
+    }
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
@@ -1347,7 +1384,7 @@ int mdx_copy_probe(size_t bytes, int iters) {
 
 int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* out, int cap) {
     if (!c || !out) return MATMUL_DECODER_ERR_INVALID_ARG;
-    if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    if (!c->persist_head) return MATMUL_DECODER_ERR_UNSUPPORTED;
     int rc = step_checks(c, token_id, NULL);
     if (rc) return rc;
     const int ev = mdx_persist_trace_events(c->L);
@@ -1381,6 +1418,6 @@ int mdx_debug_persist_spin_limit(MatmulDecoderContext* c, unsigned rounds) {
 
 int mdx_decode_path(const MatmulDecoderContext* c) {
     if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
-    return c->persist ? 1 : 0;
+    return c->persist ? (c->persist_head ? 1 : 2) : 0;
 }
 const char* mdx_last_error(void) { return mdxrt_last_error(); }

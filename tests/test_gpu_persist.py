@@ -44,7 +44,7 @@ def models(mdx, workdir):
     return cfg, get
 
 
-def _pair(mdx, oracle_lib, cfg, path, quant, persist=True):
+def _pair(mdx, oracle_lib, cfg, path, quant, persist=True, shape=SHAPE, want_path=1):
     old = os.environ.get("MDX_PERSIST")
     os.environ["MDX_PERSIST"] = "1" if persist else "0"
     try:
@@ -54,8 +54,8 @@ def _pair(mdx, oracle_lib, cfg, path, quant, persist=True):
             del os.environ["MDX_PERSIST"]
         else:
             os.environ["MDX_PERSIST"] = old
-    assert g.path == (1 if persist else 0)
-    o = oracle_lib.Model(path, SHAPE, quant, MAX_SEQ, kv_fp16=True)
+    assert g.path == (want_path if persist else 0)
+    o = oracle_lib.Model(path, shape, quant, MAX_SEQ, kv_fp16=True)
     return g, o
 
 
@@ -131,6 +131,59 @@ def test_greedy_tokens_match_oracle(mdx, gpu, oracle_lib, models, quant):
     print(f"q{quant}: gpu {toks_g}\n    oracle {toks_o}\n    min margin {min(margins):.3g}")
     assert list(toks_g) == list(toks_o)
     assert g.seq_len == 316
+
+
+def test_multi_head_layers_in_one_launch(mdx, gpu, oracle_lib, workdir):
+    """Several lm_heads (the Code Predictor form): the layers run as one launch
+    and step_head's head as a per-stage GEMV after it.  Checked against the
+    oracle and the per-stage path per step, with a token and an uploaded
+    embedding as input and heads chosen out of order."""
+    shape = dict(SHAPE, num_lm_heads=3, lm_head_vocab_size=512, vocab_size=1000,
+                 tie_word_embeddings=0)
+    cfg = mdx.qwen3_0_6b_config(name="persist-multihead", **shape)
+    path = os.path.join(workdir, "persist_multihead")
+    mdx.write_model(path, cfg, 0, 3100)
+    g1, o = _pair(mdx, oracle_lib, cfg, path, 0, shape=shape, want_path=2)
+    g0, _ = _pair(mdx, oracle_lib, cfg, path, 0, persist=False, shape=shape)
+    for m in (g1, g0):
+        m.kv_fill_normal(300, 12)
+    assert o.kv_fill_normal(300, 12) == 0
+    emb = mdx.synth_fill_normal(1024, mdx.synth_seed(12, "persist/mh-emb")) * 0.05
+    for i, head in enumerate((0, 2, 1, 2)):
+        e = emb if i == 1 else None
+        t1, l1 = g1.step_head(10 + i, head, embedding=e)
+        t0, l0 = g0.step_head(10 + i, head, embedding=e)
+        to, lo = o.step_head(10 + i, head, embedding=e, n_logits=512)
+        print(f"head {head}: one-launch {t1} per-stage {t0} oracle {to} "
+              f"cos {cosine(l1, lo):.7f} rel {rel_err(l1, lo):.2e}")
+        assert cosine(l1, lo) >= 0.9999 and rel_err(l1, lo) <= 2e-3 and t1 == to
+        assert t1 == t0 and cosine(l1, l0) >= 0.99999 and rel_err(l1, l0) <= 1e-3
+    assert g1.seq_len == g0.seq_len == 304
+    kg, vg = g1.kv_read(1, 300, 4)
+    ko, vo = o.kv_read(1, 300, 4)
+    assert np.allclose(kg, ko, rtol=4e-3, atol=4e-3) and np.allclose(vg, vo, rtol=4e-3, atol=4e-3)
+
+
+def test_fp16_lm_head_layers_in_one_launch(mdx, gpu, oracle_lib, models):
+    """disable_npu_lm_head (the fp16 lm_head): layers in one launch, then the
+    fp16 head; steps and the device greedy loop against the oracle."""
+    shape = dict(SHAPE, disable_npu_lm_head=1)
+    _, get = models
+    path = get(0)
+    cfg = mdx.qwen3_0_6b_config(name="persist-fp16-head", **shape)
+    g, o = _pair(mdx, oracle_lib, cfg, path, 0, shape=shape, want_path=2)
+    g.kv_fill_normal(200, 4)
+    assert o.kv_fill_normal(200, 4) == 0
+    for tok in (4321, 7):
+        tg, lg = g.step(tok)
+        to, lo = o.step(tok)
+        print(f"fp16 head tok {tok}: gpu {tg} oracle {to} cos {cosine(lg, lo):.7f}")
+        assert cosine(lg, lo) >= 0.9999 and rel_err(lg, lo) <= 2e-3 and tg == to
+    toks_g, _ = g.generate_greedy(100, 12)
+    toks_o, margins = o.greedy(100, 12)
+    print(f"fp16 head greedy: gpu {toks_g}\n    oracle {toks_o}\n    min margin {min(margins):.3g}")
+    assert list(toks_g) == list(toks_o)
+    assert g.seq_len == 214
 
 
 def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models, capfd):
