@@ -15,8 +15,8 @@
 // 16-bit epoch, written with agent-coherent stores and polled with
 // L2-bypassing (sc1) 16-byte loads.  A reader knows a word is current when
 // its epoch matches, so there is no flag, fence or barrier round trip.  The
-// weights of the next stage are requested before each wait, so the HBM
-// stream runs while workgroups wait for each other.
+// weights of later stages are requested ahead, mostly just after a wait, so
+// the HBM stream runs while workgroups wait for each other.
 //
 // Work split (b = workgroup, t = thread):
 //   qkv    group j = b % 8 (one KV head), split s = b / 8: the 16 rows
@@ -749,13 +749,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         MDX_TRACE(16 * l + 4);
 
-        // Waves 1..3 request their remaining gate/up and down weights now; wave 0
-        // does so after the merge, so that nothing queues in front of its poll.
         uint4 wF[SF::NW];
-        if (wave != 0) {
-            rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
-            cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
-        }
 
         // ================= C: merge the 32 partials of KV head j (wave 0) ==========
         // lane i < 32 holds split i; lanes 32..63 poll the same words and add nothing
@@ -789,17 +783,19 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 ll_put4(rs, W_ATT + (lane >> 1) * QD + (2 * j + hh) * HD + d0 + 4 * (lane & 1), pk);
             }
         }
-        if (wave == 0) {
-            rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
-            cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
-        }
+        // The remaining gate/up and the down weights are requested once the
+        // merge is done, by every wave: a burst issued while the partial
+        // records are in flight delays them (measured: 522 -> 510 us/token
+        // against requesting from waves 1..3 before the merge).
+        __syncthreads();
+        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+        cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
         MDX_TRACE(16 * l + 5);
 
         // ================= D: o projection + residual ==========
         const float sclD = Ly.so ? Ly.so[4 * b + (t & 3)] : 1.0f;
         {
-            // waves 1 and 2 gather the attention output (wave 0's weight
-            // requests were issued last)
+            // waves 1 and 2 gather the attention output
             bool ok = true;
             if (wave == 1 || wave == 2) {
                 const int u = t - 64;
