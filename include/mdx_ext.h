@@ -70,9 +70,8 @@ int mdx_step_token(MatmulDecoderContext* ctx, int token_id, const float* embeddi
 int mdx_kv_fill_normal(MatmulDecoderContext* ctx, int n_pos, uint64_t seed);
 /* Read KV rows [pos0, pos0+n) of one layer as fp32 [n][kv_heads*head_dim]. */
 int mdx_kv_read(const MatmulDecoderContext* ctx, int layer, int pos0, int n, float* k, float* v);
-/* Batch prefill of M rows, then final norm + lm_head on the last row
- * (BASELINE config 4's "lm_head on the last token only").  Writes logits
- * when non-NULL and returns the argmax. */
+/* Batch prefill of M rows, then final norm + lm_head on the last row only.
+ * Writes logits when non-NULL and returns the argmax. */
 int mdx_prefill_logits(MatmulDecoderContext* ctx, const float* embeddings, int M, float* logits);
 /* n_steps greedy tokens starting from token `first_token`, with each argmax
  * fed back on the device (no host round trip between steps).  Tokens go to

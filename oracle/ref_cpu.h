@@ -93,7 +93,8 @@ typedef struct {
 } orc_config;
 
 /* quant: 0 fp16, 1 int8, 2 int4.  kv_fp16: 1 rounds K/V to fp16 when they
- * are written (the configs' fp16 cache), 0 keeps fp32 (the reference). */
+ * are written (as the GPU decoder's fp16 cache does), 0 keeps fp32 (the
+ * reference). */
 orc_model* orc_model_open(const char* dir, const orc_config* cfg, int quant, int max_seq,
                           int kv_fp16);
 void orc_model_close(orc_model* m);

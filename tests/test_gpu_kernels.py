@@ -10,7 +10,7 @@ from conftest import cosine, rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3          # north-star bound per projection
+TOL = 1e-3          # bound per projection
 
 
 def _f16_bits(a):
