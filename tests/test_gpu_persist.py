@@ -133,7 +133,8 @@ def test_greedy_tokens_match_oracle(mdx, gpu, oracle_lib, models, quant):
     assert g.seq_len == 316
 
 
-def test_multi_head_layers_in_one_launch(mdx, gpu, oracle_lib, workdir):
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_multi_head_layers_in_one_launch(mdx, gpu, oracle_lib, workdir, quant):
     """Several lm_heads (the Code Predictor form): the layers run as one launch
     and step_head's head as a per-stage GEMV after it.  Checked against the
     oracle and the per-stage path per step, with a token and an uploaded
@@ -141,10 +142,10 @@ def test_multi_head_layers_in_one_launch(mdx, gpu, oracle_lib, workdir):
     shape = dict(SHAPE, num_lm_heads=3, lm_head_vocab_size=512, vocab_size=1000,
                  tie_word_embeddings=0)
     cfg = mdx.qwen3_0_6b_config(name="persist-multihead", **shape)
-    path = os.path.join(workdir, "persist_multihead")
-    mdx.write_model(path, cfg, 0, 3100)
-    g1, o = _pair(mdx, oracle_lib, cfg, path, 0, shape=shape, want_path=2)
-    g0, _ = _pair(mdx, oracle_lib, cfg, path, 0, persist=False, shape=shape)
+    path = os.path.join(workdir, f"persist_multihead_q{quant}")
+    mdx.write_model(path, cfg, quant, 3100 + quant)
+    g1, o = _pair(mdx, oracle_lib, cfg, path, quant, shape=shape, want_path=2)
+    g0, _ = _pair(mdx, oracle_lib, cfg, path, quant, persist=False, shape=shape)
     for m in (g1, g0):
         m.kv_fill_normal(300, 12)
     assert o.kv_fill_normal(300, 12) == 0
@@ -156,7 +157,12 @@ def test_multi_head_layers_in_one_launch(mdx, gpu, oracle_lib, workdir):
         to, lo = o.step_head(10 + i, head, embedding=e, n_logits=512)
         print(f"head {head}: one-launch {t1} per-stage {t0} oracle {to} "
               f"cos {cosine(l1, lo):.7f} rel {rel_err(l1, lo):.2e}")
-        assert cosine(l1, lo) >= 0.9999 and rel_err(l1, lo) <= 2e-3 and t1 == to
+        assert cosine(l1, lo) >= 0.9999 and rel_err(l1, lo) <= 2e-3
+        # same argmax, or a near tie: when the GPU ranks t1 above the
+        # oracle's token, the oracle's gap between them is at most twice the
+        # largest logit error
+        err = float(np.max(np.abs(l1 - lo)))
+        assert t1 == to or lo[to] - lo[t1] <= 2 * err, (t1, to, float(lo[to] - lo[t1]), err)
         assert t1 == t0 and cosine(l1, l0) >= 0.99999 and rel_err(l1, l0) <= 1e-3
     assert g1.seq_len == g0.seq_len == 304
     kg, vg = g1.kv_read(1, 300, 4)
