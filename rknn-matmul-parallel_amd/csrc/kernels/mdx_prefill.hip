@@ -279,6 +279,11 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
 // is NULL).  grid = M rows, 256 threads.
 constexpr int kMaxSplits = 16;
 
+// R > 0: N == 1024 * R, thread t owns columns 4t..4t+3 (+1024 per round), and
+// its hidden values stay in registers between the sum and the norm; the norm
+// weights are requested with the partials, so the block waits for memory once.
+// R == 0: any N (a multiple of 4), rounds looped at run time.
+template <int R>
 __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns, int N,
                                                        const float* scale, float* hidden,
                                                        const float* norm_w, float eps,
@@ -287,9 +292,13 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
     const int m = blockIdx.x, tid = threadIdx.x;
     float* hr = hidden + (size_t)m * N;
     float ss = 0.0f;
-    // thread t owns columns 4t..4t+3 (+1024 per round); every load of a round
-    // is issued before any of them is used
-    for (int c = 4 * tid; c < N; c += 1024) {
+    constexpr int RK = R > 0 ? R : 1;
+    float4 hv[RK], nwv[RK];
+    // every load of a round is issued before any of them is used
+#pragma unroll
+    for (int r = 0, c = 4 * tid; R > 0 ? r < R : c < N; r++, c += 1024) {
+        const int ri = R > 0 ? r : 0;
+        if (norm_w) nwv[ri] = *reinterpret_cast<const float4*>(norm_w + c);
         float4 p[kMaxSplits];
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; sp++)
@@ -305,6 +314,7 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
         float4 h;
         h.x = h0.x + y.x * sc.x; h.y = h0.y + y.y * sc.y; h.z = h0.z + y.z * sc.z; h.w = h0.w + y.w * sc.w;
         *reinterpret_cast<float4*>(hr + c) = h;
+        hv[ri] = h;
         ss += h.x * h.x + h.y * h.y + h.z * h.z + h.w * h.w;
     }
     if (!norm_w) return;
@@ -313,9 +323,10 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
     __syncthreads();
     const float tot = ws[0] + ws[1] + ws[2] + ws[3];
     const float rms = 1.0f / sqrtf(tot / (float)N + eps);
-    for (int c = 4 * tid; c < N; c += 1024) {
-        const float4 h = *reinterpret_cast<const float4*>(hr + c);
-        const float4 w = *reinterpret_cast<const float4*>(norm_w + c);
+#pragma unroll
+    for (int r = 0, c = 4 * tid; R > 0 ? r < R : c < N; r++, c += 1024) {
+        const float4 h = R > 0 ? hv[r] : *reinterpret_cast<const float4*>(hr + c);
+        const float4 w = R > 0 ? nwv[r] : *reinterpret_cast<const float4*>(norm_w + c);
         uint2 o;
         o.x = (uint32_t)f32_to_f16_bits((h.x * rms) * w.x) | ((uint32_t)f32_to_f16_bits((h.y * rms) * w.y) << 16);
         o.y = (uint32_t)f32_to_f16_bits((h.z * rms) * w.z) | ((uint32_t)f32_to_f16_bits((h.w * rms) * w.w) << 16);
@@ -636,8 +647,11 @@ int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w
     const int ns = residual_splits(w->N, w->K);
     int rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_residual_norm, dim3(M), dim3(256), 0, (hipStream_t)stream, scratch, ns, w->N,
-                       w->scale, hidden, norm_w, eps, x16_out);
+    const int R = w->N % 1024 == 0 ? w->N / 1024 : 0;
+    auto kern = R == 1 ? k_residual_norm<1> : R == 2 ? k_residual_norm<2> : R == 4 ? k_residual_norm<4>
+                                                                                  : k_residual_norm<0>;
+    hipLaunchKernelGGL(kern, dim3(M), dim3(256), 0, (hipStream_t)stream, scratch, ns, w->N, w->scale,
+                       hidden, norm_w, eps, x16_out);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
