@@ -50,7 +50,7 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
 // Block = 4 waves (one per SIMD, so each may hold 512 registers), one 64 x 32 output tile (all M rows, two 16-column MFMA
 // tiles; for SwiGLU the gate and up columns of the same 16 features).  The K
 // range is split over the waves in contiguous runs of K-blocks; a wave keeps
-// two rounds of K-blocks of weights and activations in flight in registers (the MFMA
+// several rounds of K-blocks of weights and activations in flight in registers (the MFMA
 // fragments are loaded straight from memory, the int8/int4 weights widened to
 // fp16 exactly in registers), so a block's loads are not serialised behind
 // barriers.  The 4 partial tiles are summed in LDS in wave order, then the
@@ -62,11 +62,14 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
 // k g*EPL + 8s .. +7; the activations are loaded with the same k mapping.
 
 template <int KIND> struct GemmKind;
-// NKB K-blocks per round; two rounds are in flight (the next one is requested
-// before the current one is multiplied).
-template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 8; };
-template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 4; };
-template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 2; };
+// NKB K-blocks per round; DEPTH rounds are in flight (a round is requested
+// DEPTH-1 rounds ahead of the one being multiplied).  Measured on the M=60
+// prefill: small rounds three deep beat larger rounds two deep (fp16
+// NKB 8 -> 1: 1.58 -> 1.43 ms; int8 NKB 4 -> 1 and depth 3: 1.366 -> 1.331
+// ms); int4 keeps two K-blocks per round (one: 1.205 -> 1.254 ms).
+template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 1, DEPTH = 3; };
+template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 1, DEPTH = 3; };
+template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 2, DEPTH = 2; };
 
 constexpr int kGemmWaves = 4;
 
@@ -218,14 +221,19 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
         for (int r = 0; r < 4; r++) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     if (kb0 < kb1) {
-        GemmRound<KIND> ra, rb;
-        gemm_issue<KIND>(ra, kb0, kb1 - 1, wrow, wvalid, arow, g);
-        for (int kb = kb0; kb < kb1; kb += 2 * GK::NKB) {
-            const int kb_b = kb + GK::NKB, kb_a2 = kb + 2 * GK::NKB;
-            if (kb_b < kb1) gemm_issue<KIND>(rb, kb_b, kb1 - 1, wrow, wvalid, arow, g);
-            gemm_compute<KIND>(ra, kb, kb1, acc);
-            if (kb_a2 < kb1) gemm_issue<KIND>(ra, kb_a2, kb1 - 1, wrow, wvalid, arow, g);
-            if (kb_b < kb1) gemm_compute<KIND>(rb, kb_b, kb1, acc);
+        constexpr int DP = GK::DEPTH;
+        GemmRound<KIND> r[DP];
+#pragma unroll
+        for (int d = 0; d < DP - 1; d++)
+            if (kb0 + d * GK::NKB < kb1) gemm_issue<KIND>(r[d], kb0 + d * GK::NKB, kb1 - 1, wrow, wvalid, arow, g);
+        for (int kb = kb0; kb < kb1; kb += DP * GK::NKB) {
+#pragma unroll
+            for (int d = 0; d < DP; d++) {
+                // request the round DP-1 ahead into the buffer freed last, then multiply round d
+                const int ki = kb + (d + DP - 1) * GK::NKB;
+                if (ki < kb1) gemm_issue<KIND>(r[(d + DP - 1) % DP], ki, kb1 - 1, wrow, wvalid, arow, g);
+                if (kb + d * GK::NKB < kb1) gemm_compute<KIND>(r[d], kb + d * GK::NKB, kb1, acc);
+            }
         }
     }
 
