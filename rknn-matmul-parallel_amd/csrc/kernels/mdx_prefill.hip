@@ -64,12 +64,12 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
 template <int KIND> struct GemmKind;
 // NKB K-blocks per round; DEPTH rounds are in flight (a round is requested
 // DEPTH-1 rounds ahead of the one being multiplied).  Measured on the M=60
-// prefill: small rounds three deep beat larger rounds two deep (fp16
-// NKB 8 -> 1: 1.58 -> 1.43 ms; int8 NKB 4 -> 1 and depth 3: 1.366 -> 1.331
-// ms); int4 keeps two K-blocks per round (one: 1.205 -> 1.254 ms).
+// prefill: small rounds three deep beat larger rounds two deep (fp16 8
+// K-blocks -> 1: 1.58 -> 1.43 ms; int8 4 -> 1: 1.366 -> 1.331 ms; int4
+// 2 -> 1: 1.206 -> 1.190 ms).
 template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 1, DEPTH = 3; };
 template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 1, DEPTH = 3; };
-template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 2, DEPTH = 2; };
+template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 1, DEPTH = 3; };
 
 constexpr int kGemmWaves = 4;
 
