@@ -47,13 +47,15 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
 
 // ---- projections: register-direct MFMA GEMM ----------------------------------
 //
-// Block = 4 waves (one per SIMD, so each may hold 512 registers), one 64 x 32 output tile (all M rows, two 16-column MFMA
-// tiles; for SwiGLU the gate and up columns of the same 16 features).  The K
+// Block = GemmKind::WAVES waves (8: two per SIMD with up to 256 registers
+// each), one 64 x 32 output tile (all M
+// rows, two 16-column MFMA tiles; for SwiGLU the gate and up columns of the
+// same 16 features).  The K
 // range is split over the waves in contiguous runs of K-blocks; a wave keeps
 // several rounds of K-blocks of weights and activations in flight in registers (the MFMA
 // fragments are loaded straight from memory, the int8/int4 weights widened to
 // fp16 exactly in registers), so a block's loads are not serialised behind
-// barriers.  The 4 partial tiles are summed in LDS in wave order, then the
+// barriers.  The waves' partial tiles are summed in LDS in wave order, then the
 // scale and the epilogue are applied.
 //
 // K-block layout: a weight load is 16 bytes per lane = EPL consecutive k of
@@ -63,15 +65,16 @@ __global__ void k_to_f16(const float* x, int n, uint16_t* x16) {
 
 template <int KIND> struct GemmKind;
 // NKB K-blocks per round; DEPTH rounds are in flight (a round is requested
-// DEPTH-1 rounds ahead of the one being multiplied).  Measured on the M=60
-// prefill: small rounds three deep beat larger rounds two deep (fp16 8
-// K-blocks -> 1: 1.58 -> 1.43 ms; int8 4 -> 1: 1.366 -> 1.331 ms; int4
-// 2 -> 1: 1.206 -> 1.190 ms).
-template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 1, DEPTH = 3; };
-template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 1, DEPTH = 3; };
-template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 1, DEPTH = 3; };
+// DEPTH-1 rounds ahead of the one being multiplied); WAVES waves per block
+// share the K range.  Measured on the M=60 prefill: small rounds three deep
+// beat larger rounds two deep (fp16 8 K-blocks -> 1: 1.58 -> 1.43 ms; int8
+// 4 -> 1: 1.366 -> 1.331 ms; int4 2 -> 1: 1.206 -> 1.190 ms), and 8 waves
+// beat 4 (int8: 1.331 -> 1.227 ms; fp16 1.43 -> 1.31 ms; int4, two rounds
+// deep to fit 256 registers: 1.188 -> 1.139 ms).
+template <> struct GemmKind<MDX_W_F16> { static constexpr int EPL = 8, NKB = 1, DEPTH = 3, WAVES = 8; };
+template <> struct GemmKind<MDX_W_I8> { static constexpr int EPL = 16, NKB = 1, DEPTH = 3, WAVES = 8; };
+template <> struct GemmKind<MDX_W_I4> { static constexpr int EPL = 32, NKB = 1, DEPTH = 2, WAVES = 8; };
 
-constexpr int kGemmWaves = 4;
 
 // Weight row of tile column c: 32 consecutive rows, or for SwiGLU the 16 gate
 // rows f0.. and the 16 up rows N/2+f0.. of the same features.
@@ -168,14 +171,15 @@ __device__ __forceinline__ void gemm_compute(const GemmRound<KIND>& R, int kb, i
 // for k_residual_norm; with part == NULL gridDim.y is 1 and the epilogue
 // writes out_f32 / out_f16.
 template <int KIND>
-__global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, int M,
+__global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm(const uint16_t* x16, int M,
                                                           const uint8_t* w, int K, int N,
                                                           const float* scale, int epi,
                                                           float* out_f32, uint16_t* out_f16,
                                                           float* part) {
     using GK = GemmKind<KIND>;
     constexpr int EPL = GK::EPL, KB = 4 * EPL;
-    __shared__ float red[kGemmWaves][kMaxM * kNT];
+    constexpr int NW = GK::WAVES;
+    __shared__ float red[NW][kMaxM * kNT];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tile = blockIdx.x;
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
     const int per_split = (nkb_all + gridDim.y - 1) / gridDim.y;
     const int sb0 = min(nkb_all, (int)blockIdx.y * per_split);
     const int sb1 = min(nkb_all, sb0 + per_split);
-    const int per = (sb1 - sb0 + kGemmWaves - 1) / kGemmWaves;
+    const int per = (sb1 - sb0 + NW - 1) / NW;
     const int kb0 = min(sb1, sb0 + wave * per), kb1 = min(sb1, kb0 + per);
 
     const uint8_t* wrow_[2];
@@ -199,7 +203,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
                                      x16 + (size_t)min(32 + c16, M - 1) * K, x16 + (size_t)min(48 + c16, M - 1) * K};
 
     // The epilogue's outputs of this thread all lie in column tid % kNT (2048
-    // outputs, 256 threads): its scales are requested now, not after the sums.
+    // outputs over a multiple of kNT threads): its scales are requested now,
+    // not after the sums.
     float sc_a = 1.0f, sc_b = 1.0f;
     if (!part && scale) {
         const int col = tid % kNT;
@@ -247,12 +252,12 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
                 red[wave][(16 * r + 4 * g + i) * kNT + 16 * t + c16] = acc[t][r][i];
     __syncthreads();
     // 2048 outputs over 256 threads, summed in wave order
-    for (int o = tid; o < kMaxM * kNT; o += kGemmWaves * 64) {
+    for (int o = tid; o < kMaxM * kNT; o += NW * 64) {
         const int row = o / kNT, col = o % kNT;
         if (row >= M) continue;
         float v = red[0][o];
 #pragma unroll
-        for (int wv = 1; wv < kGemmWaves; wv++) v = v + red[wv][o];
+        for (int wv = 1; wv < NW; wv++) v = v + red[wv][o];
         if (part) {
             const int n = tile * kNT + col;
             if (n < N) store_wt(&part[((size_t)blockIdx.y * kMaxM + row) * N + n], v);
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void k_gemm(const uint16_t* x16, i
             if (f >= cols) continue;
             float u = red[0][row * kNT + col + kNT / 2];
 #pragma unroll
-            for (int wv = 1; wv < kGemmWaves; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
+            for (int wv = 1; wv < NW; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
             const float gs = v * sc_a, us = u * sc_b;
             float act;
             if (f < (cols & ~3)) act = silu_mul(gs, us);
@@ -619,7 +624,9 @@ static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilo
     if (part ? (ns < 1 || out != nullptr) : (ns != 1 || out == nullptr)) return -1;
     if (epilogue == 2 && w->N % 2) return -1;
     dim3 grid(gemm_tiles(w->N, epilogue == 2), ns);
-    dim3 block(kGemmWaves * 64);
+    const int waves = w->kind == MDX_W_F16 ? GemmKind<MDX_W_F16>::WAVES
+                      : w->kind == MDX_W_I8 ? GemmKind<MDX_W_I8>::WAVES : GemmKind<MDX_W_I4>::WAVES;
+    dim3 block(waves * 64);
     const uint8_t* wp = (const uint8_t*)w->w;
     float* of = (float*)out;
     uint16_t* oh = (uint16_t*)out;
