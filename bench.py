@@ -161,14 +161,19 @@ def main() -> int:
     bytes_step = step_bytes(d, positions)
     log(f"decode: {ms_per_step * 1000:.1f} us/token wall, {dev_ms * 1000 / args.steps:.1f} us/token device")
 
-    # API-level latency: matmul_decoder_step with logits copied to the host each token
+    # API-level latency: matmul_decoder_step with the logits copied to the host each
+    # token, into one caller-owned buffer (a fresh array per step would add the
+    # first-touch page faults of 607 KB to every step)
     api_ms = None
     if not args.probe:
+        dec.kv_fill_normal(KV_PREFILL, 1003)
+        logits = np.empty(d["vocab_size"], np.float32)
+        dec.step_into(START_TOKEN, logits)   # untimed: the first logits copy sets up the copy path
         dec.kv_fill_normal(KV_PREFILL, 1003)
         tok, t0 = START_TOKEN, time.perf_counter()
         n_api = min(args.steps, 32)
         for _ in range(n_api):
-            tok, _ = dec.step(tok)
+            tok = dec.step_into(tok, logits)
         api_ms = round((time.perf_counter() - t0) * 1000.0 / n_api, 4)
 
     # per-projection kernels of the per-stage path (each launch cycles through

@@ -318,6 +318,13 @@ class Decoder:
         tok = lib().matmul_decoder_step(self.h, token, _p(e, _F), _p(out, _F))
         return tok, out
 
+    def step_into(self, token: int, out: np.ndarray, embedding=None) -> int:
+        """matmul_decoder_step writing the logits into a caller-owned float32 buffer
+        (reused across steps, as a C caller would)."""
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size >= self.V
+        e = _f32(embedding)
+        return lib().matmul_decoder_step(self.h, token, _p(e, _F), _p(out, _F))
+
     def step_token(self, token: int = 0, embedding=None) -> int:
         e = _f32(embedding)
         return lib().mdx_step_token(self.h, token, _p(e, _F))
