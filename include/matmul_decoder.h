@@ -293,8 +293,13 @@ int matmul_decoder_generate(MatmulDecoderContext* ctx,
  * "max_batch_prefill" are read in addition to the reference's keys. */
 int matmul_decoder_load_config(const char* json_path, MatmulDecoderConfig* config);
 
-/* Declared but never defined by the reference (include/matmul_decoder.h:467);
- * returns MATMUL_DECODER_ERR_UNSUPPORTED (exporting needs the HF toolchain). */
+/* Declared but never defined by the reference (include/matmul_decoder.h:467).
+ * Converts a local HuggingFace checkpoint (config.json + *.safetensors, F32/
+ * F16/BF16, sharded or not) into the on-disk format the loader reads, with
+ * the projections as fp16 [K,N] (QUANT_FP16) or quantised files (QUANT_INT8,
+ * QUANT_INT4); the file layout follows the reference exporter
+ * examples/qwen3_asr/export_weights.py:128-216.  Returns 0 or a negative
+ * MatmulDecoderError. */
 int matmul_decoder_export_hf_model(const char* hf_model_path,
                                    const char* output_dir,
                                    QuantizationType quant_type);

@@ -109,11 +109,3 @@ int matmul_decoder_load_config(const char* json_path, MatmulDecoderConfig* confi
     return MATMUL_DECODER_OK;
 }
 
-int matmul_decoder_export_hf_model(const char* hf_model_path, const char* output_dir,
-                                   QuantizationType quant_type) {
-    (void)hf_model_path;
-    (void)output_dir;
-    (void)quant_type;
-    fprintf(stderr, "[MatmulDecoder] export_hf_model is not available in the C library\n");
-    return MATMUL_DECODER_ERR_UNSUPPORTED;
-}

@@ -21,6 +21,10 @@ double md_now_ms(void);
 void* md_read_file(const char* path, size_t bytes);
 float* md_read_f32_first(const char* dir, const char* const* names, size_t n);
 int md_write_file(const char* path, const void* data, size_t bytes);
+/* One projection from fp32 [K,N] to <name>.bin (quant 0: fp16 [K,N]) or
+ * <name>_weight.bin + <name>_scales.bin (1: int8, 2: int4), in the layouts
+ * md_synth.c documents. */
+int md_write_proj(const char* dir, const char* name, int K, int N, int quant, const float* w);
 
 /* One projection after loading, in the on-disk semantic:
  * kind 0 fp16 [K,N], 1 int8 [K,N], 2 int4 [K,N/2]; scale may be NULL. */

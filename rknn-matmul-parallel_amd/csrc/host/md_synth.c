@@ -39,60 +39,69 @@ static int write_ones(const char* path, int n) {
     return rc;
 }
 
+/* Writes one projection given as fp32 [K,N] in the format above (quant 0
+ * fp16, 1 int8, 2 int4); shared with the checkpoint exporter. */
+int md_write_proj(const char* dir, const char* name, int K, int N, int quant, const float* w) {
+    const size_t kn = (size_t)K * N;
+    char path[1024];
+    int rc = 0;
+    if (quant == 0) {
+        uint16_t* h = (uint16_t*)malloc(kn * 2);
+        if (!h) return -1;
+        for (size_t i = 0; i < kn; i++) h[i] = mdx_f32_to_f16(w[i]);
+        snprintf(path, sizeof path, "%s/%s.bin", dir, name);
+        rc = md_write_file(path, h, kn * 2);
+        free(h);
+        return rc;
+    }
+    if (quant == 2 && N % 2) return -1;
+    float* sc = (float*)malloc((size_t)N * 4);
+    float* amax = (float*)calloc((size_t)N, 4);
+    const size_t qbytes = quant == 1 ? kn : kn / 2;
+    uint8_t* q = (uint8_t*)calloc(qbytes, 1);
+    if (!sc || !amax || !q) rc = -1;
+    for (int k = 0; !rc && k < K; k++)
+        for (int n = 0; n < N; n++) {
+            const float a = fabsf(w[(size_t)k * N + n]);
+            if (a > amax[n]) amax[n] = a;
+        }
+    for (int n = 0; !rc && n < N; n++) {
+        if (quant == 1) sc[n] = amax[n] / 127.0f;
+        else sc[n] = mdx_f16_to_f32(mdx_f32_to_f16(amax[n] / 7.0f));
+    }
+    for (int k = 0; !rc && k < K; k++) {
+        for (int n = 0; n < N; n++) {
+            const float v = w[(size_t)k * N + n];
+            if (quant == 1) {
+                const float inv = amax[n] > 0 ? 127.0f / amax[n] : 0.0f;
+                int qi = (int)roundf(v * inv);
+                qi = qi < -128 ? -128 : (qi > 127 ? 127 : qi);
+                q[(size_t)k * N + n] = (uint8_t)(int8_t)qi;
+            } else {
+                int qi = sc[n] > 0 ? (int)roundf(v / sc[n]) : 0;
+                qi = qi < -8 ? -8 : (qi > 7 ? 7 : qi);
+                uint8_t* b = &q[(size_t)k * (N / 2) + (n >> 1)];
+                *b |= (uint8_t)(((unsigned)qi & 0xfu) << ((n & 1) ? 4 : 0));
+            }
+        }
+    }
+    snprintf(path, sizeof path, "%s/%s_weight.bin", dir, name);
+    if (!rc) rc = md_write_file(path, q, qbytes);
+    snprintf(path, sizeof path, "%s/%s_scales.bin", dir, name);
+    if (!rc) rc = md_write_file(path, sc, (size_t)N * 4);
+    free(sc);
+    free(amax);
+    free(q);
+    return rc;
+}
+
 static int write_proj(const char* dir, const char* name, int K, int N, int quant, uint64_t seed,
                       const char* stream_name) {
     const size_t kn = (size_t)K * N;
     float* w = (float*)malloc(kn * 4);
     if (!w) return -1;
     mdx_synth_fill_normal(w, kn, mdx_synth_seed(seed, stream_name), 0.0, 0.02);
-    char path[1024];
-    int rc = 0;
-    if (quant == 0) {
-        uint16_t* h = (uint16_t*)malloc(kn * 2);
-        if (!h) rc = -1;
-        for (size_t i = 0; !rc && i < kn; i++) h[i] = mdx_f32_to_f16(w[i]);
-        snprintf(path, sizeof path, "%s/%s.bin", dir, name);
-        if (!rc) rc = md_write_file(path, h, kn * 2);
-        free(h);
-    } else {
-        float* sc = (float*)malloc((size_t)N * 4);
-        float* amax = (float*)calloc((size_t)N, 4);
-        const size_t qbytes = quant == 1 ? kn : kn / 2;
-        uint8_t* q = (uint8_t*)calloc(qbytes, 1);
-        if (!sc || !amax || !q) rc = -1;
-        for (int k = 0; !rc && k < K; k++)
-            for (int n = 0; n < N; n++) {
-                const float a = fabsf(w[(size_t)k * N + n]);
-                if (a > amax[n]) amax[n] = a;
-            }
-        for (int n = 0; !rc && n < N; n++) {
-            if (quant == 1) sc[n] = amax[n] / 127.0f;
-            else sc[n] = mdx_f16_to_f32(mdx_f32_to_f16(amax[n] / 7.0f));
-        }
-        for (int k = 0; !rc && k < K; k++) {
-            for (int n = 0; n < N; n++) {
-                const float v = w[(size_t)k * N + n];
-                if (quant == 1) {
-                    const float inv = amax[n] > 0 ? 127.0f / amax[n] : 0.0f;
-                    int qi = (int)roundf(v * inv);
-                    qi = qi < -128 ? -128 : (qi > 127 ? 127 : qi);
-                    q[(size_t)k * N + n] = (uint8_t)(int8_t)qi;
-                } else {
-                    int qi = sc[n] > 0 ? (int)roundf(v / sc[n]) : 0;
-                    qi = qi < -8 ? -8 : (qi > 7 ? 7 : qi);
-                    uint8_t* b = &q[(size_t)k * (N / 2) + (n >> 1)];
-                    *b |= (uint8_t)(((unsigned)qi & 0xfu) << ((n & 1) ? 4 : 0));
-                }
-            }
-        }
-        snprintf(path, sizeof path, "%s/%s_weight.bin", dir, name);
-        if (!rc) rc = md_write_file(path, q, qbytes);
-        snprintf(path, sizeof path, "%s/%s_scales.bin", dir, name);
-        if (!rc) rc = md_write_file(path, sc, (size_t)N * 4);
-        free(sc);
-        free(amax);
-        free(q);
-    }
+    const int rc = md_write_proj(dir, name, K, N, quant, w);
     free(w);
     return rc;
 }

@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
     constexpr int RK = R > 0 ? R : 1;
     float4 hv[RK], nwv[RK];
     // every load of a round is issued before any of them is used
-#pragma unroll
+#pragma unroll RK
     for (int r = 0, c = 4 * tid; R > 0 ? r < R : c < N; r++, c += 1024) {
         const int ri = R > 0 ? r : 0;
         if (norm_w) nwv[ri] = *reinterpret_cast<const float4*>(norm_w + c);
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
     __syncthreads();
     const float tot = ws[0] + ws[1] + ws[2] + ws[3];
     const float rms = 1.0f / sqrtf(tot / (float)N + eps);
-#pragma unroll
+#pragma unroll RK
     for (int r = 0, c = 4 * tid; R > 0 ? r < R : c < N; r++, c += 1024) {
         const float4 h = R > 0 ? hv[r] : *reinterpret_cast<const float4*>(hr + c);
         const float4 w = R > 0 ? nwv[r] : *reinterpret_cast<const float4*>(norm_w + c);

@@ -131,6 +131,7 @@ def lib() -> C.CDLL:
             "mdx_f16_to_f32": (C.c_float, [C.c_uint16]),
             "mdx_synth_seed": (C.c_uint64, [C.c_uint64, C.c_char_p]),
             "mdx_synth_fill_normal": (None, [_F, C.c_size_t, C.c_uint64, C.c_double, C.c_double]),
+            "matmul_decoder_export_hf_model": (C.c_int, [C.c_char_p, C.c_char_p, C.c_int]),
             "mdx_synth_write_model": (C.c_int, [C.c_char_p, C.POINTER(MatmulDecoderConfig), C.c_int,
                                                 C.c_uint64]),
         }
@@ -182,6 +183,17 @@ def quantize_lm_head(lm16, V: int, K: int):
     s = np.empty(V, np.float32)
     lib().mdx_quantize_lm_head(_p(q, _I8), _p(s, _F), _p(lm16, _U16), V, K)
     return q.reshape(V, K), s
+
+
+QUANT_NAMES = {"fp16": 0, "int8": 1, "int4": 2, "int4_g128": 3}
+
+
+def export_hf_model(hf_dir: str, out_dir: str, quant: str = "fp16") -> None:
+    """matmul_decoder_export_hf_model: a local HuggingFace checkpoint
+    (config.json + *.safetensors) to the reference on-disk format."""
+    rc = lib().matmul_decoder_export_hf_model(hf_dir.encode(), out_dir.encode(), QUANT_NAMES[quant])
+    if rc != 0:
+        raise RuntimeError(f"matmul_decoder_export_hf_model failed ({rc})")
 
 
 def write_model(path: str, cfg: MatmulDecoderConfig, quant: int, seed: int) -> None:

@@ -15,6 +15,7 @@ from conftest import PKG, cosine, rel_err, tiny_config
 pytestmark = pytest.mark.gpu
 
 QNAME = {0: "fp16", 1: "int8", 2: "int4"}
+QNAME_TO_Q = {v: k for k, v in QNAME.items()}
 
 
 @pytest.fixture(scope="module")
@@ -121,6 +122,32 @@ def test_multi_head_step_head(mdx, gpu, oracle_lib, workdir):
         to, lo = o.step_head(10 + i, head, n_logits=200)
         assert tg == to and rel_err(lg, lo) < 1e-3
     assert g.step_head(1, 3)[0] == -1 and g.step_head(1, -1)[0] == -1
+
+
+@pytest.mark.parametrize("quant", ["fp16", "int8", "int4"])
+def test_exported_hf_checkpoint_matches_oracle(mdx, gpu, oracle_lib, workdir, quant):
+    """A HuggingFace-layout checkpoint (BF16 safetensors in two shards, tiny
+    Qwen3 shape) exported by matmul_decoder_export_hf_model and loaded by the
+    decoder from the exported config.json, against the oracle reading the same
+    files: 8 greedy steps, logits and tokens."""
+    import json
+    te = pytest.importorskip("test_export_cpu")
+    hf = dict(hidden_size=128, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+              intermediate_size=256, num_hidden_layers=2, vocab_size=512, rms_norm_eps=1e-6,
+              rope_theta=1000000.0)
+    hf_dir = os.path.join(workdir, f"gpu_hf_ckpt_{quant}")
+    te._write_checkpoint(hf_dir, te._tensors(hf, seed=11), hf)
+    out = os.path.join(workdir, f"gpu_hf_export_{quant}")
+    mdx.export_hf_model(hf_dir, out, quant)
+    d = json.load(open(os.path.join(out, "config.json")))
+    g = mdx.Decoder(out, None, quant, 64)
+    o = oracle_lib.Model(out, d, QNAME_TO_Q[quant], 64, kv_fp16=True)
+    tg = to = 7
+    for step in range(8):
+        tg, lg = g.step(tg)
+        to, lo = o.step(to)
+        assert rel_err(lg, lo) < 1e-3 and cosine(lg, lo) > 0.9999, f"step {step}"
+        assert tg == to, f"step {step}"
 
 
 def test_error_returns(mdx, gpu, models):
