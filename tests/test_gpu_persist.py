@@ -192,6 +192,37 @@ def test_fp16_lm_head_layers_in_one_launch(mdx, gpu, oracle_lib, models):
     assert g.seq_len == 214
 
 
+def test_create_destroy_cycles_release_device_memory(mdx, gpu, oracle_lib, models):
+    """Contexts of the one-launch shape created, stepped (token, greedy loop,
+    prefill) and destroyed ten times: the device's free memory returns to
+    where it started (within 64 MiB of runtime caching)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    free_b, total_b = ctypes.c_size_t(0), ctypes.c_size_t(0)
+
+    def free_now():
+        assert hip.hipMemGetInfo(ctypes.byref(free_b), ctypes.byref(total_b)) == 0
+        return free_b.value
+
+    cfg, get = models
+    path = get(1)
+    g = mdx.Decoder(path, cfg, "int8", 256)     # first context: runtime set-up outside the count
+    g.step(3)
+    g.close()
+    before = free_now()
+    emb = np.random.default_rng(3).standard_normal((20, 1024)).astype(np.float32)
+    for i in range(10):
+        g = mdx.Decoder(path, cfg, "int8", 256)
+        assert g.path == 1
+        g.step(3 + i)
+        g.generate_greedy(5, 4)
+        assert g.prefill_batch(emb) == 0
+        g.close()
+    after = free_now()
+    print(f"free before {before >> 20} MiB, after {after >> 20} MiB")
+    assert before - after < (64 << 20)
+
+
 def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models, capfd):
     """A one-launch step whose waits give up (forced here with a 1-round spin
     limit, as a grid that is not co-resident would) reports the timeout in the
