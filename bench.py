@@ -59,11 +59,14 @@ def model_dir(mdx, tag: str, cfg, quant: int, seed: int) -> str:
     return path
 
 
-def step_bytes(d: dict, positions: list[int]) -> float:
-    """Algorithmic HBM bytes of one decode step (weights + lm_head + KV), mean over positions."""
+def step_bytes(d: dict, positions: list[int], quant: int = 0) -> float:
+    """Algorithmic HBM bytes of one decode step (weights + lm_head + KV), mean over positions.
+    quant 0: fp16 layer weights; 2: int4 weights plus fp32 per-row scales."""
     h, qd, kvd, F, L, V = d["hidden_dim"], d["num_q_heads"] * d["head_dim"], \
         d["num_kv_heads"] * d["head_dim"], d["ffn_dim"], d["num_layers"], d["vocab_size"]
-    layer_w = 2.0 * (h * (qd + 2 * kvd) + qd * h + 2 * h * F + F * h)
+    elems = h * (qd + 2 * kvd) + qd * h + 2 * h * F + F * h
+    rows = (qd + 2 * kvd) + h + 2 * F + h
+    layer_w = 2.0 * elems if quant == 0 else 0.5 * elems + 4.0 * rows
     norms = 4.0 * (2 * h + 2 * d["head_dim"])
     lm = V * h * 1.0 + V * 4.0
     kv = np.mean([L * (p + 1) * kvd * 2 * 2.0 for p in positions])
@@ -115,12 +118,19 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--workload", default="fp16_kv512", choices=["fp16_kv512", "w4a16_kv4096"],
+                    help="decode workload: fp16 layers at KV 512 (the default line), or W4A16 at "
+                         "KV 4096 (decode only)")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (the calibration kernel), then the "
                          "decode steps only")
     args = ap.parse_args()
     if args.probe:
         args.no_prefill = args.no_cpu_baseline = True
+    w4 = args.workload == "w4a16_kv4096"
+    if w4:
+        args.no_prefill = args.no_cpu_baseline = True
+    kv0 = 4096 if w4 else KV_PREFILL
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs the decoder on a single MI355X and has "
               "no multi-GPU path (see DESIGN.md for how it would shard); use --gpus 1.",
@@ -135,8 +145,10 @@ def main() -> int:
     d = dict(hidden_dim=1024, num_q_heads=16, num_kv_heads=8, head_dim=128, ffn_dim=3072,
              num_layers=28, vocab_size=151936, max_seq_len=4096, rms_eps=1e-6, rope_theta=1e6,
              tie_word_embeddings=1, has_qk_norm=1, rope_style=1, max_batch_prefill=64)
+    if w4:
+        d["max_seq_len"] = 4224
     cfg = mdx.qwen3_0_6b_config(name="qwen3-0.6b-synthetic", **d)
-    max_seq = KV_PREFILL + max(args.steps, args.warmup) + 8
+    max_seq = kv0 + max(args.steps, args.warmup) + 8
 
     if args.probe:
         # plain copy of a known size: the scale for the HBM byte counters
@@ -146,19 +158,20 @@ def main() -> int:
         log("probe copy: 3 x 256 MiB device-to-device")
 
     # ---- decode (config: 28-layer greedy, FP16 layers + INT8 lm_head, KV 512) ----
-    path16 = model_dir(mdx, "decode_fp16_seed1003", cfg, 0, 1003)
+    path16 = model_dir(mdx, "decode_int4_seed1005" if w4 else "decode_fp16_seed1003", cfg,
+                       2 if w4 else 0, 1005 if w4 else 1003)
     t0 = time.time()
-    dec = mdx.Decoder(path16, cfg, "fp16", max_seq)
+    dec = mdx.Decoder(path16, cfg, "int4" if w4 else "fp16", max_seq)
     log(f"decoder created in {time.time() - t0:.1f}s")
-    dec.kv_fill_normal(KV_PREFILL, 1003)
+    dec.kv_fill_normal(kv0, 1003)
     dec.generate_greedy(START_TOKEN, args.warmup)
-    dec.kv_fill_normal(KV_PREFILL, 1003)
+    dec.kv_fill_normal(kv0, 1003)
     t0 = time.perf_counter()
     toks, dev_ms = dec.generate_greedy(START_TOKEN, args.steps)
     wall_s = time.perf_counter() - t0
     ms_per_step = wall_s * 1000.0 / args.steps
-    positions = list(range(KV_PREFILL, KV_PREFILL + args.steps))
-    bytes_step = step_bytes(d, positions)
+    positions = list(range(kv0, kv0 + args.steps))
+    bytes_step = step_bytes(d, positions, 2 if w4 else 0)
     log(f"decode: {ms_per_step * 1000:.1f} us/token wall, {dev_ms * 1000 / args.steps:.1f} us/token device")
 
     # API-level latency: matmul_decoder_step with the logits copied to the host each
@@ -166,10 +179,10 @@ def main() -> int:
     # first-touch page faults of 607 KB to every step)
     api_ms = None
     if not args.probe:
-        dec.kv_fill_normal(KV_PREFILL, 1003)
+        dec.kv_fill_normal(kv0, 1003)
         logits = np.empty(d["vocab_size"], np.float32)
         dec.step_into(START_TOKEN, logits)   # untimed: the first logits copy sets up the copy path
-        dec.kv_fill_normal(KV_PREFILL, 1003)
+        dec.kv_fill_normal(kv0, 1003)
         tok, t0 = START_TOKEN, time.perf_counter()
         n_api = min(args.steps, 32)
         for _ in range(n_api):
@@ -179,7 +192,7 @@ def main() -> int:
     # per-projection kernels of the per-stage path (each launch cycles through
     # the 28 layers' weights)
     kernels = {}
-    for name, per_step in () if args.probe else (("qkv", 28), ("o", 28), ("gate_up", 28),
+    for name, per_step in () if args.probe or w4 else (("qkv", 28), ("o", 28), ("gate_up", 28),
                                                  ("down", 28), ("lm_head", 1)):
         iters = 280 if per_step == 28 else 40
         dec.time_projection(name, 28)
@@ -191,7 +204,7 @@ def main() -> int:
     step_us = dev_ms * 1000.0 / args.steps
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "k_persist_step_fp16_decode_kv512_traffic.json")
-    if os.path.exists(tfile):
+    if os.path.exists(tfile) and not w4:
         with open(tfile) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
@@ -229,15 +242,16 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "i4 x f16" if w4 else "f16",
         "data": "synthetic (seeded random-init Qwen3-0.6B-shaped weights and N(0,1) KV)",
-        "config": {"workload": "28-layer greedy decode, fp16 layers + int8 lm_head, fp16 KV 512->576, "
-                               "1 token per step, argmax fed back on device",
+        "config": {"workload": f"28-layer greedy decode, {'int4 (W4A16)' if w4 else 'fp16'} layers + "
+                               f"int8 lm_head, fp16 KV {kv0}->{kv0 + args.steps}, 1 token per step, "
+                               "argmax fed back on device",
                    "hidden": 1024, "heads": "16q/8kv x128", "ffn": 3072, "vocab": 151936,
-                   "kv_start": KV_PREFILL, "start_token": START_TOKEN},
+                   "kv_start": kv0, "start_token": START_TOKEN},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_persist_step<f16> (one launch per token: 28 layers + "
-                               "INT8 lm_head + argmax)" if path_kind == 1 else
+                     "kernel": f"k_persist_step<{'i4' if w4 else 'f16'}> (one launch per token: 28 "
+                               "layers + INT8 lm_head + argmax)" if path_kind == 1 else
                                "per-stage kernel sequence (one-launch step unavailable)",
                      "achieved": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
