@@ -537,11 +537,10 @@ static int run_prefill(MatmulDecoderContext* c, int M, void* s) {
     for (int l = 0; l < c->L && rc == 0; l++) {
         md_layer* ly = &c->layers[l];
         const float* next_norm = l + 1 < c->L ? c->layers[l + 1].in_norm : NULL;
-        rc = mdx_launch_gemm(c->d_bx16, M, &ly->qkv, 0, c->d_bqkv, c->d_gscr, s);
-        if (!rc)
-            rc = mdx_launch_qk_rope_append_rows(c->d_state, c->d_bqkv, M, ly->q_norm, ly->k_norm,
-                                                eps, c->d_cos, c->d_sin, c->nq, c->nkv, c->hd,
-                                                c->config.rope_style, c->d_bq, ly->kc, ly->vc, s);
+        /* qkv as K-split partials, summed by the RoPE/append kernel */
+        rc = mdx_launch_qkv_rope_append_rows(c->d_bx16, M, &ly->qkv, c->d_gscr, c->d_state, ly->q_norm,
+                                             ly->k_norm, eps, c->d_cos, c->d_sin, c->nq, c->nkv, c->hd,
+                                             c->config.rope_style, c->d_bq, ly->kc, ly->vc, s);
         if (!rc)
             rc = mdx_launch_attn_prefill(c->d_state, c->d_bq, M, ly->kc, ly->vc, c->nq, c->nkv,
                                          c->hd, c->d_battn16, s);

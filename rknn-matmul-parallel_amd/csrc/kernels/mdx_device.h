@@ -216,6 +216,16 @@ int mdx_launch_qk_rope_append_rows(const mdx_state* state, const float* qkv, int
                                    int hd, int rope_style, float* q_out, uint16_t* k_cache,
                                    uint16_t* v_cache, void* stream);
 
+/* The qkv projection and the launch above in one call: X16 . W^T as K-split
+ * partials in scratch (mdx_gemm_scratch_floats(M, N, K) floats, about 256
+ * blocks so every CU takes a share), which the QK-norm/RoPE/append kernel
+ * sums in split order and scales per column as it reads the rows. */
+int mdx_launch_qkv_rope_append_rows(const uint16_t* x16, int M, const mdx_wdesc* w, float* scratch,
+                                    const mdx_state* state, const float* q_norm, const float* k_norm,
+                                    float eps, const float* cos_t, const float* sin_t, int nq, int nkv,
+                                    int hd, int rope_style, float* q_out, uint16_t* k_cache,
+                                    uint16_t* v_cache, void* stream);
+
 /* Causal attention for query rows t < M at positions state->pos + t over
  * cache rows [0, state->pos + t]; output fp16 [M][nq*hd]. */
 int mdx_launch_attn_prefill(const mdx_state* state, const float* q, int M,

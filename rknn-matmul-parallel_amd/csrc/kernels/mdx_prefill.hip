@@ -352,23 +352,38 @@ __global__ __launch_bounds__(256) void k_residual_norm(const float* part, int ns
 // grid = (nq + 2*nkv, M), 64 threads; hd <= 256 (at most two pairs per lane).
 constexpr int kRopePairs = 2;
 __global__ __launch_bounds__(64) void k_qk_rope_append_rows(
-    const mdx_state* st, const float* qkv, const float* q_norm, const float* k_norm, float eps,
-    const float* cos_t, const float* sin_t, int nq, int nkv, int hd, int style, float* q_out,
-    uint16_t* k_cache, uint16_t* v_cache) {
+    const mdx_state* st, const float* qkv, const float* part, int ns, const float* pscale,
+    const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+    int nq, int nkv, int hd, int style, float* q_out, uint16_t* k_cache, uint16_t* v_cache) {
     const int b = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int pos = st->pos + t;
     const int half = hd / 2;
-    const int qd = nq * hd, kvd = nkv * hd;
-    const float* row = qkv + (size_t)t * (qd + 2 * kvd);
+    const int qd = nq * hd, kvd = nkv * hd, nn = qd + 2 * kvd;
+    // this block's head: columns [c0, c0 + hd) of the row
+    const int c0 = b < nq ? b * hd : (b < nq + nkv ? qd + (b - nq) * hd : qd + kvd + (b - nq - nkv) * hd);
+    __shared__ float rowv[2 * 64 * kRopePairs];
+    const float* slice;
+    if (part) {
+        // the qkv GEMM's K-split partials, summed in split order, times the column scale
+        for (int e = lane; e < hd; e += 64) {
+            float v = part[(size_t)t * nn + c0 + e];
+            for (int sp = 1; sp < ns; sp++) v = v + part[((size_t)sp * kMaxM + t) * nn + c0 + e];
+            rowv[e] = pscale ? v * pscale[c0 + e] : v;
+        }
+        __syncthreads();
+        slice = rowv;
+    } else {
+        slice = qkv + (size_t)t * nn + c0;
+    }
     if (b >= nq + nkv) {
         const int h = b - nq - nkv;
-        const float* src = row + qd + kvd + h * hd;
+        const float* src = slice;
         uint16_t* dst = v_cache + (size_t)pos * kvd + h * hd;
         for (int e = lane; e < hd; e += 64) dst[e] = f32_to_f16_bits(src[e]);
         return;
     }
     const bool is_q = b < nq;
-    const float* src = is_q ? row + b * hd : row + qd + (b - nq) * hd;
+    const float* src = slice;
     const float* nw = is_q ? q_norm : k_norm;
     const float* cr = cos_t + (size_t)pos * half;
     const float* sr = sin_t + (size_t)pos * half;
@@ -677,8 +692,23 @@ int mdx_launch_qk_rope_append_rows(const mdx_state* state, const float* qkv, int
                                    uint16_t* v_cache, void* stream) {
     if (hd % 2 || hd > 2 * 64 * kRopePairs || M <= 0) return -1;
     hipLaunchKernelGGL(k_qk_rope_append_rows, dim3(nq + 2 * nkv, M), dim3(64), 0, (hipStream_t)stream,
-                       state, qkv, q_norm, k_norm, eps, cos_t, sin_t, nq, nkv, hd, rope_style, q_out,
-                       k_cache, v_cache);
+                       state, qkv, (const float*)nullptr, 0, (const float*)nullptr, q_norm, k_norm, eps,
+                       cos_t, sin_t, nq, nkv, hd, rope_style, q_out, k_cache, v_cache);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int mdx_launch_qkv_rope_append_rows(const uint16_t* x16, int M, const mdx_wdesc* w, float* scratch,
+                                    const mdx_state* state, const float* q_norm, const float* k_norm,
+                                    float eps, const float* cos_t, const float* sin_t, int nq, int nkv,
+                                    int hd, int rope_style, float* q_out, uint16_t* k_cache,
+                                    uint16_t* v_cache, void* stream) {
+    if (hd % 2 || hd > 2 * 64 * kRopePairs || M <= 0 || w->N != (nq + 2 * nkv) * hd) return -1;
+    const int ns = residual_splits(w->N, w->K);
+    int rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_qk_rope_append_rows, dim3(nq + 2 * nkv, M), dim3(64), 0, (hipStream_t)stream,
+                       state, (const float*)nullptr, (const float*)scratch, ns, w->scale, q_norm, k_norm,
+                       eps, cos_t, sin_t, nq, nkv, hd, rope_style, q_out, k_cache, v_cache);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
