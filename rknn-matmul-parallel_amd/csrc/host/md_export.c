@@ -210,7 +210,7 @@ static int st_add_file(st_set* s, const char* path) {
                 p = js_ws(p);
                 if (*p == ',') p++;
             }
-            if (!p || !have_offs || offs[1] < offs[0]) { rc = MATMUL_DECODER_ERR_FILE_IO; break; }
+            if (!p || !have_offs || offs[0] < 0 || offs[1] < offs[0]) { rc = MATMUL_DECODER_ERR_FILE_IO; break; }
             t.begin = (unsigned long long)offs[0];
             t.end = (unsigned long long)offs[1];
             t.file = fi;
@@ -314,7 +314,10 @@ static float* st_read_f32(const st_set* s, const char* name, size_t count) {
     if (!t) return NULL;
     if (t->ndim > 4) return NULL;
     size_t elems = 1;
-    for (int i = 0; i < t->ndim; i++) elems *= (size_t)t->shape[i];
+    for (int i = 0; i < t->ndim; i++) {
+        if (t->shape[i] < 0 || t->shape[i] > (1ll << 32)) return NULL;
+        elems *= (size_t)t->shape[i];
+    }
     const size_t esz = t->dtype == ST_F32 ? 4 : 2;
     if (t->dtype < 0 || elems != count || t->end - t->begin != elems * esz) {
         fprintf(stderr, "[MatmulDecoder] export: %s has an unexpected dtype or shape\n", t->name);
@@ -420,9 +423,12 @@ static int hf_read_config(const char* dir, hf_config* c) {
     hf_scan(text, c, 0);
     free(text);
     if (c->head_dim <= 0 && c->heads > 0) c->head_dim = c->hidden / c->heads;
+    const long long lim = 1ll << 22;   /* keeps every product below in int range */
     if (c->hidden <= 0 || c->heads <= 0 || c->kv_heads <= 0 || c->head_dim <= 0 || c->ffn <= 0 ||
-        c->layers <= 0 || c->vocab <= 0) {
-        fprintf(stderr, "[MatmulDecoder] export: %s lacks a model dimension\n", path);
+        c->layers <= 0 || c->vocab <= 0 || c->hidden > 65536 || c->ffn > 262144 ||
+        c->heads * c->head_dim > 65536 || c->kv_heads * c->head_dim > 65536 || c->layers > 4096 ||
+        c->vocab > lim) {
+        fprintf(stderr, "[MatmulDecoder] export: %s lacks a model dimension or has one out of range\n", path);
         return MATMUL_DECODER_ERR_INVALID_ARG;
     }
     return MATMUL_DECODER_OK;

@@ -173,6 +173,21 @@ def test_export_errors_and_cli(mdx, workdir):
     _write_checkpoint(broken, tensors, HF, shards=1)
     with pytest.raises(RuntimeError):
         mdx.export_hf_model(broken, os.path.join(workdir, "export_broken"), "fp16")
+    # a dimension out of range, and a header with a negative data offset
+    huge = os.path.join(workdir, "hf_huge")
+    _write_checkpoint(huge, _tensors(HF, seed=6), dict(HF, hidden_size=1 << 40), shards=1)
+    with pytest.raises(RuntimeError):
+        mdx.export_hf_model(huge, os.path.join(workdir, "export_huge"), "fp16")
+    bad = os.path.join(workdir, "hf_bad_header")
+    os.makedirs(bad, exist_ok=True)
+    with open(os.path.join(bad, "config.json"), "w") as f:
+        json.dump(HF, f)
+    hdr = json.dumps({"model.embed_tokens.weight": {"dtype": "F32", "shape": [1, 1],
+                                                    "data_offsets": [-8, 4]}}).encode()
+    with open(os.path.join(bad, "model.safetensors"), "wb") as f:
+        f.write(len(hdr).to_bytes(8, "little") + hdr + bytes(4))
+    with pytest.raises(RuntimeError):
+        mdx.export_hf_model(bad, os.path.join(workdir, "export_bad_header"), "fp16")
     # the command line
     hf_dir = os.path.join(workdir, "hf_cli")
     tensors = _tensors(HF, seed=5)
