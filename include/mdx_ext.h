@@ -127,6 +127,44 @@ int mdx_debug_qk_rope(int nq, int nkv, int hd, int pos, int rope_style, float th
 int mdx_debug_lmhead(int lm_kind, int K, int N, const void* w_rows, const float* scales,
                      const float* hidden, const float* norm_w, float eps, float* logits);
 
+/* Runs the sampler of matmul_decoder_step_sample on host logits[V]
+ * (uploaded, penalised, sampled, copied back).  out[0] = token, out[1] =
+ * candidates kept after top-p; top_idx/top_val (may be NULL) receive the k
+ * candidates, k = clamp(top_k, 1, V), by descending tempered value.
+ * Returns 0 or a negative error. */
+int mdx_debug_sample(const float* logits, int V, const SamplingParams* params, float uniform,
+                     int* out, int* top_idx, float* top_val);
+
+/* ---- device-side sampling ---------------------------------------------- */
+
+#define MDX_SAMPLE_MAX_REPEAT 4096
+
+/* One decode step (as matmul_decoder_step with a logits buffer) followed by
+ * sampling on the device from the logits it leaves in HBM, so non-greedy
+ * decoding copies no logits to the host (output_logits may be NULL; when
+ * given it receives the step's logits before the penalty).  Reference:
+ * src/cpu_ops.c:593-648 (top_k_sample_f32) and the SamplingParams of
+ * include/matmul_decoder.h:391-398, with these definitions:
+ *   - repeat_penalty p != 1: each distinct listed token's logit l becomes
+ *     l / p if l > 0, else l * p (the reference declares the field and
+ *     applies it nowhere);
+ *   - temperature T: v = l / T when T != 1, as the reference divides;
+ *   - top_k k = clamp(top_k, 1, V), at most MDX_SAMPLE_MAX_TOP_K: the k
+ *     largest v, ties to the lower index, in descending order;
+ *     e_j = expf(v_j - v_0), summed in that order;
+ *   - top_p < 1: only the shortest prefix whose running sum reaches
+ *     top_p * sum is kept (the reference's top_p_sample_f32 returns the
+ *     argmax instead);
+ *   - uniform u in [0,1] replaces rand() / RAND_MAX: r = u * sum, the token
+ *     is the first candidate whose running sum exceeds r, else the last.
+ * top_k <= 1 gives the argmax of the penalised, tempered logits.  Returns
+ * the token, or a negative error (INVALID_ARG for out-of-range parameters
+ * or repeat tokens, more than MDX_SAMPLE_MAX_REPEAT of them, or a bad
+ * token/full cache as matmul_decoder_step; UNSUPPORTED for a context with
+ * several lm_heads).  Not part of the reference ABI. */
+int matmul_decoder_step_sample(MatmulDecoderContext* ctx, int token_id, const float* embedding,
+                               const SamplingParams* params, float uniform, float* output_logits);
+
 /* ---- host helpers shared with tools (no GPU needed) ---- */
 
 /* INT8 lm_head quantiser of the reference (per vocab row of the fp16 copy):

@@ -21,6 +21,7 @@ _F = C.POINTER(C.c_float)
 _U16 = C.POINTER(C.c_uint16)
 _I8 = C.POINTER(C.c_int8)
 _U8 = C.POINTER(C.c_uint8)
+_I32 = C.POINTER(C.c_int32)
 
 
 class OrcConfig(C.Structure):
@@ -62,6 +63,8 @@ def lib() -> C.CDLL:
             "orc_silu_mul": (None, [_F, _F, _F, C.c_int]),
             "orc_vec_add": (None, [_F, _F, C.c_int]),
             "orc_argmax": (C.c_int, [_F, C.c_int]),
+            "orc_sample_topk": (C.c_int, [_F, C.c_int, _I32, C.c_int, C.c_float, C.c_int, C.c_float,
+                                          C.c_float, C.c_float, _I32, _F, _I32]),
             "orc_matmul_f16": (None, [_F, _F, _U16, C.c_int, C.c_int, C.c_int]),
             "orc_set_accum_order": (None, [C.c_int]),
             "orc_matmul_i8": (None, [_F, _F, _I8, _F, C.c_int, C.c_int, C.c_int]),
@@ -178,6 +181,23 @@ def silu_mul(g, u) -> np.ndarray:
 def argmax(x) -> int:
     x = _f32(x)
     return lib().orc_argmax(_p(x, _F), x.size)
+
+
+def sample_topk(logits, top_k=1, temperature=1.0, top_p=1.0, u=0.0, repeat_tokens=(),
+                repeat_penalty=1.0):
+    """Top-k sampling with the given uniform (src/cpu_ops.c:593-648 with u in
+    place of rand()/RAND_MAX); top_k is clamped to [1, V].  Returns (token,
+    candidate indices, candidate values after temperature, kept after top-p)."""
+    x = np.array(logits, dtype=np.float32, copy=True).ravel()
+    k = max(1, min(int(top_k), x.size))
+    rep = np.ascontiguousarray(np.asarray(repeat_tokens, dtype=np.int32).ravel())
+    idx = np.zeros(k, np.int32)
+    val = np.zeros(k, np.float32)
+    kept = np.zeros(1, np.int32)
+    tok = lib().orc_sample_topk(_p(x, _F), x.size, _p(rep, _I32), rep.size, float(repeat_penalty), k,
+                                float(temperature), float(top_p), float(u), _p(idx, _I32),
+                                _p(val, _F), _p(kept, _I32))
+    return tok, idx, val, int(kept[0])
 
 
 # ---- projections -------------------------------------------------------------

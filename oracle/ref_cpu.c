@@ -311,6 +311,91 @@ int orc_argmax(const float* x, int n) {
     return mi;
 }
 
+/* Sampling.  Reference: src/cpu_ops.c:593-648 (top_k_sample_f32), with the
+ * caller's uniform u in [0,1] in place of rand() / RAND_MAX so that a draw is
+ * reproducible.  Steps the reference does not define (it declares
+ * repeat_penalty in include/matmul_decoder.h:395-397 and applies it nowhere;
+ * its top_p_sample_f32, src/cpu_ops.c:650-665, returns the argmax) follow the
+ * device sampler's definitions:
+ *   - penalty p != 1: each distinct listed token's logit l -> l > 0 ? l / p : l * p;
+ *   - top_p < 1: keep the shortest prefix of the sorted candidates whose
+ *     running sum of e_j reaches top_p * sum, and draw from it.
+ * x is modified (penalty, temperature).  top_idx/top_val (k each, may be
+ * NULL) receive the candidates; *kept the prefix length.  Returns the token. */
+int orc_sample_topk(float* x, int vocab_size, const int* rep, int n_rep, float penalty, int k,
+                    float temperature, float top_p, float u, int* top_idx, float* top_val, int* kept) {
+    if (penalty != 1.0f) {
+        for (int i = 0; i < n_rep; i++) {
+            int seen = 0;
+            for (int j = 0; j < i && !seen; j++) seen = rep[j] == rep[i];
+            if (seen) continue;
+            const float l = x[rep[i]];
+            x[rep[i]] = l > 0.0f ? l / penalty : l * penalty;
+        }
+    }
+    /* src/cpu_ops.c:597-601 */
+    if (temperature != 1.0f)
+        for (int i = 0; i < vocab_size; i++) x[i] /= temperature;
+    /* src/cpu_ops.c:604-624: insertion into a descending list of k */
+    int* idx = (int*)malloc((size_t)k * sizeof(int));
+    float* val = (float*)malloc((size_t)k * sizeof(float));
+    for (int i = 0; i < k; i++) {
+        val[i] = -1e30f;
+        idx[i] = 0;
+    }
+    for (int i = 0; i < vocab_size; i++) {
+        if (x[i] > val[k - 1]) {
+            int j = k - 1;
+            while (j > 0 && x[i] > val[j - 1]) {
+                val[j] = val[j - 1];
+                idx[j] = idx[j - 1];
+                j--;
+            }
+            val[j] = x[i];
+            idx[j] = i;
+        }
+    }
+    if (top_idx)
+        for (int i = 0; i < k; i++) top_idx[i] = idx[i];
+    if (top_val)
+        for (int i = 0; i < k; i++) top_val[i] = val[i];
+    /* src/cpu_ops.c:626-632: softmax over the k, summed in order */
+    const float max_val = val[0];
+    float sum = 0.0f;
+    for (int i = 0; i < k; i++) {
+        val[i] = expf(val[i] - max_val);
+        sum += val[i];
+    }
+    int m = k;
+    if (top_p < 1.0f) {
+        const float lim = top_p * sum;
+        float run = 0.0f;
+        for (int i = 0; i < k; i++) {
+            run += val[i];
+            if (run >= lim) {
+                m = i + 1;
+                break;
+            }
+        }
+        sum = run;
+    }
+    if (kept) *kept = m;
+    /* src/cpu_ops.c:634-646 */
+    const float r = u * sum;
+    float cumsum = 0.0f;
+    int result = idx[m - 1];
+    for (int i = 0; i < m; i++) {
+        cumsum += val[i];
+        if (r < cumsum) {
+            result = idx[i];
+            break;
+        }
+    }
+    free(idx);
+    free(val);
+    return result;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Projections                                                               */
 /* ------------------------------------------------------------------------ */

@@ -56,6 +56,9 @@ void orc_attention_batch_causal(float* out, const float* q_batch, const float* k
 void orc_silu_mul(float* out, const float* gate, const float* up, int dim);
 void orc_vec_add(float* dst, const float* src, int n);
 int orc_argmax(const float* x, int n);
+/* Top-k sampling with a given uniform (src/cpu_ops.c:593-648); see ref_cpu.c. */
+int orc_sample_topk(float* x, int vocab_size, const int* rep, int n_rep, float penalty, int k,
+                    float temperature, float top_p, float u, int* top_idx, float* top_val, int* kept);
 
 /* ---- projections on the reference weight layout W[K,N] row-major ---- */
 /* Projection accumulation order: 0 increasing k (default), 1 four

@@ -308,3 +308,36 @@ int mdx_debug_lmhead(int lm_kind, int K, int N, const void* w_rows, const float*
     rc = scope_close(&s, rc);
     return rc ? rc : h.argmax;
 }
+
+int mdx_debug_sample(const float* logits, int V, const SamplingParams* params, float uniform,
+                     int* out, int* top_idx, float* top_val) {
+    if (!logits || !out) return MATMUL_DECODER_ERR_INVALID_ARG;
+    int k = 1, n = 0, *toks = NULL;
+    int rc = md_sample_prepare(params, V, uniform, &k, &toks, &n);
+    if (rc) return rc;
+    dbg_scope s;
+    rc = scope_open(&s);
+    if (rc) {
+        free(toks);
+        return rc;
+    }
+    float* dl = (float*)dalloc(&s, (size_t)V * 4);
+    int* dt = n ? (int*)dalloc(&s, (size_t)n * 4) : NULL;
+    int* dout = (int*)dalloc(&s, 256);
+    int* di = (int*)dalloc(&s, (size_t)k * 4);
+    float* dv = (float*)dalloc(&s, (size_t)k * 4);
+    void* dsc = dalloc(&s, mdx_sample_scratch_bytes());
+    if (!dl || (n && !dt) || !dout || !di || !dv || !dsc) rc = MATMUL_DECODER_ERR_MEMORY;
+    if (!rc) rc = mdxrt_h2d(dl, logits, (size_t)V * 4);
+    if (!rc && n) rc = mdxrt_h2d(dt, toks, (size_t)n * 4);
+    if (!rc && n) rc = mdx_launch_repeat_penalty(dl, dt, n, params->repeat_penalty, s.stream);
+    if (!rc)
+        rc = mdx_launch_topk_sample(dl, V, params->temperature, k, params->top_p, uniform, dsc, dout, di,
+                                    dv, s.stream);
+    if (!rc) rc = mdxrt_stream_sync(s.stream);
+    if (!rc) rc = mdxrt_d2h(out, dout, 2 * sizeof(int));
+    if (!rc && top_idx) rc = mdxrt_d2h(top_idx, di, (size_t)k * 4);
+    if (!rc && top_val) rc = mdxrt_d2h(top_val, dv, (size_t)k * 4);
+    free(toks);
+    return scope_close(&s, rc);
+}

@@ -51,6 +51,7 @@ struct MatmulDecoderContext {
     uint16_t *d_kc, *d_vc;
     float *d_cos, *d_sin;
     float *d_hidden, *d_emb_in, *d_qkv, *d_logits, *d_tmp;
+    void* d_sscr;                /* sampler scratch */
     void* d_part;            /* attention split partials + merge counters */
     uint16_t *d_attn16, *d_act16;
     void* d_partial;         /* lm_head argmax key + completion counter */
@@ -72,6 +73,7 @@ struct MatmulDecoderContext {
     mdx_persist_args pargs;
     mdx_state* h_state;
     float* h_io;
+    int* h_samp;                 /* pinned: sampler tokens, then {token, kept} */
     size_t h_io_floats;
     void *ev0, *ev1, *ev2;
     MatmulDecoderStats stats;
@@ -356,6 +358,7 @@ static int layout(MatmulDecoderContext* c, const md_source* s) {
     CARVE(c->d_qkv, (size_t)(c->qd + 2 * c->kvd) * 4);
     CARVE(c->d_part, mdx_attn_decode_scratch_bytes(c->nq, c->nkv, c->hd, c->max_splits));
     CARVE(c->d_logits, (size_t)nlog * 4);
+    CARVE(c->d_sscr, mdx_sample_scratch_bytes());
     CARVE(c->d_tmp, (size_t)(widest > c->d ? widest : c->d) * 4);
     CARVE(c->d_attn16, (size_t)c->qd * 2);
     CARVE(c->d_act16, (size_t)c->F * 2);
@@ -863,6 +866,7 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     c->h_io_floats = (size_t)(c->V > c->lm_vocab ? c->V : c->lm_vocab);
     if ((size_t)c->max_m * c->d > c->h_io_floats) c->h_io_floats = (size_t)c->max_m * c->d;
     if (mdxrt_host_alloc((void**)&c->h_io, c->h_io_floats * 4)) goto fail;
+    if (mdxrt_host_alloc((void**)&c->h_samp, (MDX_SAMPLE_MAX_REPEAT + 64) * sizeof(int))) goto fail;
     memset(c->h_state, 0, sizeof(mdx_state));
     setup_persist(c);
     if (md_verbose())
@@ -945,6 +949,7 @@ void matmul_decoder_destroy(MatmulDecoderContext* c) {
     mdxrt_free(c->arena);
     mdxrt_host_free(c->h_state);
     mdxrt_host_free(c->h_io);
+    mdxrt_host_free(c->h_samp);
     mdxrt_event_destroy(c->ev0);
     mdxrt_event_destroy(c->ev1);
     mdxrt_event_destroy(c->ev2);
@@ -987,8 +992,16 @@ static int step_checks(MatmulDecoderContext* c, int token_id, const float* embed
 /* One decode step.  want_head selects the lm_head (the reference's
  * output_logits != NULL); logits_out may be NULL with want_head set when
  * only the token is needed. */
+/* A device-side draw appended to a step (matmul_decoder_step_sample): the n
+ * distinct penalised tokens are in c->h_samp[0..n). */
+typedef struct {
+    const SamplingParams* p;
+    int k, n;
+    float u;
+} md_sample_req;
+
 static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding,
-                   float* output_logits, int want_head) {
+                   float* output_logits, int want_head, const md_sample_req* sr) {
     if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
     const double t0 = md_now_ms();
     int rc = step_checks(c, token_id, embedding);
@@ -1018,6 +1031,16 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     }
     if (!rc) rc = mdxrt_event_record(c->ev2, c->stream);
     if (!rc && output_logits) rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
+    if (!rc && sr) {
+        /* penalty and draw on the logits just copied out; the kernels read
+         * the tokens from and write {token, kept} to pinned host memory */
+        if (sr->n)
+            rc = mdx_launch_repeat_penalty(c->d_logits, c->h_samp, sr->n, sr->p->repeat_penalty, c->stream);
+        if (!rc)
+            rc = mdx_launch_topk_sample(c->d_logits, c->V, sr->p->temperature, sr->k, sr->p->top_p, sr->u,
+                                        c->d_sscr, c->h_samp + MDX_SAMPLE_MAX_REPEAT, NULL, NULL,
+                                        c->stream);
+    }
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
     if (c->persist) pthread_mutex_unlock(&g_persist_mu);
@@ -1026,7 +1049,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
         return MATMUL_DECODER_ERR_RKNN;
     }
     if (c->h_state->pad[1]) {
-        if (persist_retry(c)) return do_step(c, token_id, embedding, output_logits, want_head);
+        if (persist_retry(c)) return do_step(c, token_id, embedding, output_logits, want_head, sr);
         fprintf(stderr, "[MatmulDecoder] step failed: a workgroup timed out waiting for another\n");
         return MATMUL_DECODER_ERR_RKNN;
     }
@@ -1037,6 +1060,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     int tok = 0;
     if (output_logits) memcpy(output_logits, c->h_io, (size_t)c->V * 4);
     if (want_head) tok = c->h_state->argmax;
+    if (sr) tok = c->h_samp[MDX_SAMPLE_MAX_REPEAT];
     const float total = (float)(md_now_ms() - t0);
     c->stats.total_ms = total;
     c->stats.matmul_ms = layers_ms;
@@ -1052,11 +1076,11 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
 
 int matmul_decoder_step(MatmulDecoderContext* c, int token_id, const float* embedding,
                         float* output_logits) {
-    return do_step(c, token_id, embedding, output_logits, output_logits != NULL);
+    return do_step(c, token_id, embedding, output_logits, output_logits != NULL, NULL);
 }
 
 int mdx_step_token(MatmulDecoderContext* c, int token_id, const float* embedding) {
-    return do_step(c, token_id, embedding, NULL, 1);
+    return do_step(c, token_id, embedding, NULL, 1, NULL);
 }
 
 int matmul_decoder_step_get_logits(MatmulDecoderContext* c, int token_id, const float* embedding,
@@ -1189,6 +1213,52 @@ int matmul_decoder_generate(MatmulDecoderContext* c, const int* prompt_tokens, i
 /* ------------------------------------------------------------------------ */
 /* Additive entry points (mdx_ext.h)                                         */
 /* ------------------------------------------------------------------------ */
+
+static int int_cmp(const void* a, const void* b) {
+    const int x = *(const int*)a, y = *(const int*)b;
+    return (x > y) - (x < y);
+}
+
+int md_sample_prepare(const SamplingParams* p, int V, float uniform, int* k_out, int** toks,
+                      int* n_toks) {
+    *toks = NULL;
+    *n_toks = 0;
+    if (!p || V <= 0 || !(uniform >= 0.0f && uniform <= 1.0f) || !(p->temperature > 0.0f) ||
+        !isfinite(p->temperature) || !(p->repeat_penalty > 0.0f) || !isfinite(p->repeat_penalty) ||
+        p->top_p != p->top_p || p->n_repeat_tokens < 0 || p->n_repeat_tokens > MDX_SAMPLE_MAX_REPEAT ||
+        (p->n_repeat_tokens > 0 && !p->repeat_tokens))
+        return MATMUL_DECODER_ERR_INVALID_ARG;
+    const int k = p->top_k <= 1 ? 1 : (p->top_k > V ? V : p->top_k);
+    if (k > MDX_SAMPLE_MAX_TOP_K) return MATMUL_DECODER_ERR_INVALID_ARG;
+    for (int i = 0; i < p->n_repeat_tokens; i++)
+        if (p->repeat_tokens[i] < 0 || p->repeat_tokens[i] >= V) return MATMUL_DECODER_ERR_INVALID_ARG;
+    *k_out = k;
+    if (p->repeat_penalty == 1.0f || p->n_repeat_tokens == 0) return 0;
+    /* once per distinct token */
+    int* t = (int*)malloc((size_t)p->n_repeat_tokens * sizeof(int));
+    if (!t) return MATMUL_DECODER_ERR_MEMORY;
+    memcpy(t, p->repeat_tokens, (size_t)p->n_repeat_tokens * sizeof(int));
+    qsort(t, (size_t)p->n_repeat_tokens, sizeof(int), int_cmp);
+    int n = 0;
+    for (int i = 0; i < p->n_repeat_tokens; i++)
+        if (n == 0 || t[i] != t[n - 1]) t[n++] = t[i];
+    *toks = t;
+    *n_toks = n;
+    return 0;
+}
+
+int matmul_decoder_step_sample(MatmulDecoderContext* c, int token_id, const float* embedding,
+                               const SamplingParams* params, float uniform, float* output_logits) {
+    if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
+    if (c->n_lm > 1) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    md_sample_req sr = {params, 1, 0, uniform};
+    int* toks = NULL;
+    int rc = md_sample_prepare(params, c->V, uniform, &sr.k, &toks, &sr.n);
+    if (rc) return rc;
+    if (sr.n) memcpy(c->h_samp, toks, (size_t)sr.n * sizeof(int));
+    free(toks);
+    return do_step(c, token_id, embedding, output_logits, 1, &sr);
+}
 
 int mdx_kv_fill_normal(MatmulDecoderContext* c, int n_pos, uint64_t seed) {
     if (!c || n_pos < 0 || n_pos > c->max_seq) return MATMUL_DECODER_ERR_INVALID_ARG;

@@ -43,4 +43,10 @@ int md_repack_rows(const md_host_proj* p, int dst_kind, void* dst_rows, float* d
                    int row0);
 size_t md_row_bytes(int dev_kind, int K);
 
+/* Validates SamplingParams for the device sampler: *k_out = clamp(top_k, 1,
+ * V); *toks (malloc'd, caller frees) = the distinct repeat tokens when the
+ * penalty applies, *n_toks their count. */
+int md_sample_prepare(const SamplingParams* p, int V, float uniform, int* k_out, int** toks,
+                      int* n_toks);
+
 #endif

@@ -235,6 +235,26 @@ int mdx_launch_attn_prefill(const mdx_state* state, const float* q, int M,
 /* Copy row M-1 of x[M][d] to dst[d] (last-token hidden after prefill). */
 int mdx_launch_copy_row(const float* x, int row, int d, float* dst, void* stream);
 
+/* ---- sampling (mdx_sample.hip) ---- */
+
+#define MDX_SAMPLE_MAX_TOP_K 1024
+
+/* logits[t] = logits[t] > 0 ? logits[t] / penalty : logits[t] * penalty for
+ * each of the n tokens, which must be distinct and in range. */
+int mdx_launch_repeat_penalty(float* logits, const int* tokens, int n, float penalty, void* stream);
+
+/* Device scratch of mdx_launch_topk_sample (cleared by the launch itself). */
+size_t mdx_sample_scratch_bytes(void);
+
+/* Temperature, top-k (1 <= k <= min(V, MDX_SAMPLE_MAX_TOP_K); ties to the
+ * lower index), top-p over the candidates when top_p < 1, and the draw at
+ * uniform in [0,1].  out[0] = token, out[1] = candidates kept after top-p.
+ * top_idx/top_val (k each, may be NULL) receive the candidates by descending
+ * tempered value.  Calls sharing one scratch must not overlap. */
+int mdx_launch_topk_sample(const float* logits, int V, float temperature, int k, float top_p,
+                           float uniform, void* scratch, int* out, int* top_idx, float* top_val,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

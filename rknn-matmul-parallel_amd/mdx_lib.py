@@ -46,6 +46,22 @@ class MatmulDecoderStats(C.Structure):
                 ("n_steps", C.c_int)]
 
 
+class SamplingParams(C.Structure):
+    """Mirror of SamplingParams (include/matmul_decoder.h)."""
+    _fields_ = [("top_k", C.c_int), ("top_p", C.c_float), ("temperature", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_tokens", _I), ("n_repeat_tokens", C.c_int)]
+
+
+def sampling_params(top_k=1, top_p=1.0, temperature=1.0, repeat_penalty=1.0, repeat_tokens=()):
+    """SamplingParams plus the int32 array its repeat_tokens points into (keep
+    both alive for the call)."""
+    toks = np.ascontiguousarray(np.asarray(repeat_tokens, dtype=np.int32).ravel())
+    p = SamplingParams(top_k=int(top_k), top_p=float(top_p), temperature=float(temperature),
+                       repeat_penalty=float(repeat_penalty),
+                       repeat_tokens=_p(toks, _I) if toks.size else None, n_repeat_tokens=toks.size)
+    return p, toks
+
+
 class RmpConfig(C.Structure):
     _fields_ = [("M", C.c_int), ("K", C.c_int), ("N", C.c_int), ("type", C.c_int),
                 ("layout", C.c_int), ("n_workers", C.c_int)]
@@ -126,6 +142,9 @@ def lib() -> C.CDLL:
             "mdx_debug_qk_rope": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                             C.c_float, _F, _F, _F, _F, _U16, _U16]),
             "mdx_debug_lmhead": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F, C.c_float, _F]),
+            "mdx_debug_sample": (C.c_int, [_F, C.c_int, C.POINTER(SamplingParams), C.c_float, _I, _I, _F]),
+            "matmul_decoder_step_sample": (C.c_int, [P, C.c_int, _F, C.POINTER(SamplingParams), C.c_float,
+                                                     _F]),
             "mdx_quantize_lm_head": (None, [_I8, _F, _U16, C.c_int, C.c_int]),
             "mdx_f32_to_f16": (C.c_uint16, [C.c_float]),
             "mdx_f16_to_f32": (C.c_float, [C.c_uint16]),
@@ -280,6 +299,20 @@ def lmhead(kind: int, K: int, N: int, w_rows, scales, hidden, norm_w, eps: float
     return tok, out
 
 
+def sample(logits, top_k=1, temperature=1.0, top_p=1.0, u=0.0, repeat_tokens=(), repeat_penalty=1.0):
+    """The device sampler on host logits: (token, candidate indices, candidate
+    values after temperature, kept after top-p)."""
+    x = _f32(logits).ravel()
+    p, toks = sampling_params(top_k, top_p, temperature, repeat_penalty, repeat_tokens)
+    k = max(1, min(int(top_k), x.size))
+    out = np.zeros(2, np.int32)
+    idx = np.zeros(k, np.int32)
+    val = np.zeros(k, np.float32)
+    _check(lib().mdx_debug_sample(_p(x, _F), x.size, C.byref(p), float(u), _p(out, _I), _p(idx, _I),
+                                  _p(val, _F)), "sample")
+    return int(out[0]), idx, val, int(out[1])
+
+
 # ---- decoder ---------------------------------------------------------------------
 
 class Decoder:
@@ -336,6 +369,16 @@ class Decoder:
         assert out.dtype == np.float32 and out.flags.c_contiguous and out.size >= self.V
         e = _f32(embedding)
         return lib().matmul_decoder_step(self.h, token, _p(e, _F), _p(out, _F))
+
+    def step_sample(self, token: int, u: float, top_k=1, temperature=1.0, top_p=1.0, repeat_tokens=(),
+                    repeat_penalty=1.0, embedding=None, logits: bool = False):
+        """matmul_decoder_step_sample: one step, then sampling on the device.
+        Returns (token or negative error, logits or None)."""
+        e = _f32(embedding)
+        p, toks = sampling_params(top_k, top_p, temperature, repeat_penalty, repeat_tokens)
+        out = np.empty(self.V, np.float32) if logits else None
+        tok = lib().matmul_decoder_step_sample(self.h, token, _p(e, _F), C.byref(p), float(u), _p(out, _F))
+        return tok, out
 
     def step_token(self, token: int = 0, embedding=None) -> int:
         e = _f32(embedding)
