@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 from conftest import cosine, rel_err
+from test_gpu_sample import _near_boundary
 
 pytestmark = pytest.mark.gpu
 
@@ -279,3 +280,35 @@ def test_two_contexts_in_two_threads(mdx, gpu, oracle_lib, models, capfd):
     err = capfd.readouterr().err
     assert "retrying with cooperative launches" not in err
     assert out[0] == ref[0] and out[1] == ref[1]
+
+
+def test_step_sample_after_one_launch_step(mdx, gpu, oracle_lib, models):
+    """matmul_decoder_step_sample on the one-launch path: the sampler is
+    enqueued after the persistent step and draws what the oracle's sampler
+    (src/cpu_ops.c:593-648 with the same uniform) draws from the logits the
+    same step returns; a plain-step twin fed the same tokens sees the same
+    logits at every step."""
+    cfg, get = models
+    path = get(1)
+    a, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    b, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    a.kv_fill_normal(40, 9)
+    b.kv_fill_normal(40, 9)
+    rng = np.random.default_rng(5)
+    tok = 4321
+    hist = []
+    for i in range(8):
+        u = float(rng.random())
+        kw = dict(top_k=[2, 50, 1000][i % 3], temperature=0.9, top_p=[1.0, 0.8][i % 2],
+                  repeat_tokens=hist[-4:], repeat_penalty=1.3)
+        ts, ls = a.step_sample(tok, u, logits=True, **kw)
+        _, lb = b.step(tok)
+        assert np.array_equal(ls, lb), i
+        rt, _, rval, rkept = oracle_lib.sample_topk(lb, u=u, **kw)
+        # equal, except where a last-bit expf difference can move a boundary
+        assert ts == rt or _near_boundary(rval, rkept, u, kw["top_p"]), (i, ts, rt)
+        hist.append(ts)
+        tok = ts
+    assert a.seq_len == b.seq_len == 48
+    a.close()
+    b.close()
