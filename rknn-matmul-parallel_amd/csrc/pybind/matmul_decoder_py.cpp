@@ -135,6 +135,32 @@ public:
         return mdx_step_token(ctx_, token_id, ep);
     }
 
+    // One step, then a draw on the device (matmul_decoder_step_sample); u is
+    // the caller's uniform in [0,1].  Not in the reference module.
+    int step_sample(int token_id, float u, int top_k, float top_p, float temperature,
+                    float repeat_penalty, std::vector<int> repeat_tokens, py::object embedding) {
+        FArray emb;
+        const float* ep = nullptr;
+        if (!embedding.is_none()) {
+            emb = embedding.cast<FArray>();
+            ep = row_ptr(emb);
+        }
+        SamplingParams p = sampling_params_greedy();
+        p.top_k = top_k;
+        p.top_p = top_p;
+        p.temperature = temperature;
+        p.repeat_penalty = repeat_penalty;
+        p.repeat_tokens = repeat_tokens.empty() ? nullptr : repeat_tokens.data();
+        p.n_repeat_tokens = (int)repeat_tokens.size();
+        int tok;
+        {
+            py::gil_scoped_release nogil;
+            tok = matmul_decoder_step_sample(ctx_, token_id, ep, &p, u, nullptr);
+        }
+        if (tok < 0) throw std::runtime_error("step_sample failed (" + std::to_string(tok) + ")");
+        return tok;
+    }
+
     void clear_kv_cache() { matmul_decoder_clear_kv_cache(ctx_); }
 
     int seq_len() const { return matmul_decoder_get_seq_len(ctx_); }
@@ -217,6 +243,11 @@ PYBIND11_MODULE(matmul_decoder, m) {
              "Batch prefill of M tokens, embeddings [M, hidden_dim]")
         .def("step_get_token", &PyMatmulDecoder::step_get_token, py::arg("token_id"),
              py::arg("embedding") = py::none(), "Run one decoding step, return the greedy token")
+        .def("step_sample", &PyMatmulDecoder::step_sample, py::arg("token_id"), py::arg("u"),
+             py::arg("top_k") = 40, py::arg("top_p") = 1.0f, py::arg("temperature") = 1.0f,
+             py::arg("repeat_penalty") = 1.0f, py::arg("repeat_tokens") = std::vector<int>(),
+             py::arg("embedding") = py::none(),
+             "One decoding step, then top-k/top-p sampling on the device with uniform u in [0,1]")
         .def("clear_kv_cache", &PyMatmulDecoder::clear_kv_cache, "Clear the KV cache")
         .def("generate", &PyMatmulDecoder::generate, py::arg("prompt_tokens"),
              py::arg("max_new_tokens") = 128, py::arg("top_k") = 1, py::arg("top_p") = 1.0f,

@@ -285,6 +285,23 @@ def test_pybind_module_end_to_end(mdx, gpu, oracle_lib, models):
     assert out == want
     with pytest.raises(RuntimeError):
         dec.prefill_batch(np.zeros((100, d["hidden_dim"]), np.float32))
+    # device-side sampling: the oracle's draw from the same step's logits
+    dec.clear_kv_cache()
+    o3 = oracle_lib.Model(path, d, 0, 64)
+    t = 9
+    for i, u in enumerate((0.12, 0.5, 0.93)):
+        ts = dec.step_sample(t, u, top_k=20, top_p=0.95, temperature=0.8, repeat_penalty=1.2,
+                             repeat_tokens=[t, 9])
+        _, lo = o3.step(t)
+        rt, _, rval, rkept = oracle_lib.sample_topk(lo, top_k=20, top_p=0.95, temperature=0.8, u=u,
+                                                    repeat_tokens=[t, 9], repeat_penalty=1.2)
+        # the oracle's logits differ from the device's within the projection
+        # tolerance, so a draw may differ only next to a running-sum boundary
+        run = np.cumsum(np.exp(rval.astype(np.float64) - float(rval[0])))
+        assert ts == rt or np.min(np.abs(run[:rkept] - u * run[rkept - 1])) <= 1e-2 * run[-1], (i, ts, rt)
+        t = rt
+    with pytest.raises(RuntimeError):
+        dec.step_sample(1, 2.0)
 
 
 @pytest.mark.parametrize("M", [1, 5, 64, 70])

@@ -172,7 +172,8 @@ def test_pybind_module_surface(mdx):
     sys.path.insert(0, PKG)
     import matmul_decoder as md
     assert md.__version__ == "1.0.0"
-    for name in ("step", "prefill", "prefill_batch", "step_get_token", "clear_kv_cache", "generate"):
+    for name in ("step", "prefill", "prefill_batch", "step_get_token", "clear_kv_cache", "generate",
+                 "step_sample"):
         assert hasattr(md.MatmulDecoder, name)
     for prop in ("seq_len", "config", "stats"):
         assert isinstance(getattr(md.MatmulDecoder, prop), property)
