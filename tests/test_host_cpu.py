@@ -183,3 +183,27 @@ def test_pybind_module_surface(mdx):
     if mdx.device_count() == 0:
         with pytest.raises(RuntimeError):
             md.MatmulDecoder("/nonexistent", max_seq_len=16, quant_type="fp16")
+
+
+def test_sampler_parameter_checks_run_before_any_device_call(mdx):
+    """md_sample_prepare rejects out-of-range SamplingParams with INVALID_ARG
+    (-1) before touching a device; valid ones reach the device (UNSUPPORTED,
+    -5, where there is none)."""
+    import ctypes
+    if mdx.device_count() != 0:
+        pytest.skip("checks the no-device return code")
+    L = mdx.lib()
+    x = np.zeros(2048, np.float32)        # top_k is clamped to V first, then limited to 1024
+    out = np.zeros(2, np.int32)
+
+    def call(u=0.5, **kw):
+        p, toks = mdx.sampling_params(**kw)
+        return L.mdx_debug_sample(x.ctypes.data_as(mdx._F), x.size, ctypes.byref(p), u,
+                                  out.ctypes.data_as(mdx._I), None, None)
+
+    for kw in (dict(top_k=1025), dict(temperature=0.0), dict(temperature=float("inf")),
+               dict(repeat_penalty=-1.0), dict(top_p=float("nan")), dict(repeat_tokens=[2048], repeat_penalty=1.1),
+               dict(repeat_tokens=[-1], repeat_penalty=1.1), dict(repeat_tokens=list(range(64)) * 65)):
+        assert call(**kw) == -1, kw
+    assert call(u=1.01) == -1 and call(u=-0.01) == -1
+    assert call(top_k=1000, top_p=0.9, temperature=0.7, repeat_tokens=[1, 1, 2], repeat_penalty=1.3) == -5
