@@ -266,12 +266,15 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
 
     // rank by (value desc, index asc); the pairs are distinct, so the ranks
     // are a permutation of 0..k-1
+    __shared__ uint32_t ckey[kMaxK];
+    if (tid < k) ckey[tid] = order_key(cval[tid]);
+    __syncthreads();
     if (tid < k) {
-        const uint32_t kj = order_key(cval[tid]);
+        const uint32_t kj = ckey[tid];
         const int ij = cidx[tid];
         int r = 0;
         for (int m = 0; m < k; m++) {
-            const uint32_t km = order_key(cval[m]);
+            const uint32_t km = ckey[m];
             r += km > kj || (km == kj && cidx[m] < ij);
         }
         sidx[r] = ij;
