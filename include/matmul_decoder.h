@@ -233,11 +233,25 @@ void matmul_decoder_clear_kv_cache(MatmulDecoderContext* ctx);
 int matmul_decoder_get_seq_len(const MatmulDecoderContext* ctx);
 const MatmulDecoderConfig* matmul_decoder_get_config(const MatmulDecoderContext* ctx);
 
-/* Reference: include/matmul_decoder.h:372-382.  On the GPU: total_ms is the
- * host wall time of the call, matmul_ms the projection kernels, lm_head_ms
- * the lm_head, cpu_ops_ms the fused norm/rope/attention kernels (kernel
- * times only when MDX_PROFILE=1, otherwise 0), rebind_ms is always 0 and
- * convert_ms is the host<->device copy time. */
+/* Reference: include/matmul_decoder.h:372-382, filled by step() as in
+ * src/matmul_decoder.c:1551-1560, 1616-1623 (prefill_batch and step_head
+ * leave them alone).  On the GPU, device times come from events on the
+ * step's stream:
+ *   total_ms    host wall time of the call;
+ *   matmul_ms   the projections (with the norm, residual and SwiGLU they
+ *               carry).  A step whose layers and lm_head are one launch
+ *               counts that whole launch here, unless MDX_PROFILE=1;
+ *   lm_head_ms  the lm_head when it is a kernel of its own (0 in prefill
+ *               mode and inside the one launch unless MDX_PROFILE=1);
+ *   cpu_ops_ms  QK-norm, RoPE, KV append and attention (0 unless
+ *               MDX_PROFILE=1: they are fused into the same launch);
+ *   rebind_ms   time the one launch's stages wait for each other's results
+ *               (0 unless MDX_PROFILE=1; there are no B buffers to rebind);
+ *   convert_ms  total_ms minus the device times above (uploads, copies of
+ *               the logits, launch and synchronisation).
+ * MDX_PROFILE=1 at creation times every stage of the one launch
+ * (per-workgroup timestamps, medians over workgroups, scaled to the launch's
+ * event time), at the cost of a 0.9 MB copy per step. */
 typedef struct {
     float total_ms;
     float matmul_ms;

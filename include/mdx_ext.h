@@ -50,6 +50,11 @@ int mdx_decode_path(const MatmulDecoderContext* ctx);
  * times before giving up (0: the default), which forces the timeout-and-retry
  * path without any workgroup waiting long. */
 int mdx_debug_persist_spin_limit(MatmulDecoderContext* ctx, unsigned rounds);
+/* Test hook: before the next cooperative retry, leave exchange words tagged
+ * with the epoch that retry would accept first (what a workgroup of the
+ * timed-out launch that started late could have written); the retry must
+ * clear them and still produce the undisturbed result. */
+int mdx_debug_persist_poison_retry(MatmulDecoderContext* ctx);
 
 /* One decode step of the one-launch path with per-workgroup timestamps
  * (100 MHz device clock) at every stage boundary: out[256][E] with E
@@ -81,15 +86,24 @@ int mdx_prefill_logits(MatmulDecoderContext* ctx, const float* embeddings, int M
 int mdx_generate_greedy(MatmulDecoderContext* ctx, int first_token, int n_steps, int* out_tokens,
                         float* device_ms);
 /* Average device microseconds of one launch of a layer projection kernel
- * ("qkv", "o", "gate_up", "down", "lm_head"), timed with HIP events over
- * `iters` launches cycling through all layers (distinct weights).  *bytes
- * receives the algorithmic HBM bytes of one launch. */
+ * ("qkv", "o", "gate_up", "down", "lm_head"), or of the four launches that
+ * make one layer's seven projections with their RMSNorms ("layer"), timed
+ * with HIP events over `iters` repetitions cycling through all layers
+ * (distinct weights).  *bytes receives the algorithmic HBM bytes of one
+ * repetition. */
 int mdx_time_projection(MatmulDecoderContext* ctx, const char* which, int iters, float* avg_us,
                         double* bytes);
 /* Device milliseconds of one M-row batch prefill through all layers (timed
  * with HIP events, KV position restored afterwards). */
 int mdx_time_prefill(MatmulDecoderContext* ctx, const float* embeddings, int M, int iters,
                      float* avg_ms);
+
+/* Average device microseconds of one GEMV y = fp16(x) . W (x per-column
+ * scale) with kind 1 (int8) or 0 (fp16) weights of [K,N], timed with HIP
+ * events over `iters` back-to-back launches that cycle through `copies`
+ * distinct weight buffers (enough copies defeat the device caches).  The
+ * buffers hold a fixed pattern; the kernel is the decoder's per-stage GEMV. */
+int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us);
 
 /* ---- single-kernel entry points (weights in the on-disk layout) ---- */
 

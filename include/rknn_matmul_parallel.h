@@ -48,7 +48,9 @@ typedef struct {
 typedef struct RmpContext RmpContext;
 
 /* Copies the fp16 [K,N] weights into device memory (reference:
- * src/rknn_matmul_parallel.c:200-300).  Returns NULL on failure. */
+ * src/rknn_matmul_parallel.c:200-300).  Any K >= 1 (a K that is not a
+ * multiple of 32 is zero-padded on the device); N must divide by n_workers.
+ * Returns NULL on failure. */
 RmpContext* rmp_create(const RmpConfig* config, const void* weights, const float* scales);
 
 /* output[M,N] fp32 = fp16 input[M,K] x W (reference:

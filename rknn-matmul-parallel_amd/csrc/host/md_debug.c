@@ -99,6 +99,52 @@ int mdx_debug_gemv(int kind, int K, int N, const void* w, const float* scales, c
     return scope_close(&s, rc);
 }
 
+int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us) {
+    if ((kind != 0 && kind != 1) || K <= 0 || K % 32 || N <= 0 || copies <= 0 || iters <= 0 || !avg_us)
+        return MATMUL_DECODER_ERR_INVALID_ARG;
+    if (mdxrt_device_count() <= 0) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    const int dk = kind == 0 ? MDX_W_F16 : MDX_W_I8;
+    const size_t wb = md_row_bytes(dk, K) * (size_t)N;
+    const size_t per = (wb + (size_t)N * 4 + 255) / 256 * 256;     /* weights + scales */
+    void *s = NULL, *e0 = NULL, *e1 = NULL;
+    uint8_t* buf = NULL;
+    float *dx = NULL, *dy = NULL;
+    int rc = mdxrt_stream_create(&s) || mdxrt_event_create(&e0) || mdxrt_event_create(&e1);
+    if (!rc) rc = mdxrt_malloc((void**)&buf, per * copies);
+    if (!rc) rc = mdxrt_malloc((void**)&dx, (size_t)K * 4);
+    if (!rc) rc = mdxrt_malloc((void**)&dy, (size_t)N * 4);
+    /* weight bytes 0x01, 0x3c01 as fp16 (about 1.0), scales 1/256, x 1.0 */
+    if (!rc) rc = mdxrt_fill_u32(buf, kind ? 0x01010101u : 0x3c013c01u, per * copies / 4, s);
+    for (int i = 0; i < copies && !rc; i++)
+        rc = mdxrt_fill_u32(buf + per * i + wb, 0x3b800000u, (size_t)N, s);
+    if (!rc) rc = mdxrt_fill_u32(dx, 0x3f800000u, (size_t)K, s);
+    mdx_wdesc w = {NULL, NULL, dk, K, N};
+    for (int i = 0; i < 8 && !rc; i++) {   /* warm-up */
+        w.w = buf + per * (i % copies);
+        w.scale = (const float*)(buf + per * (i % copies) + wb);
+        rc = mdx_launch_gemv(dx, &w, 0, dy, s);
+    }
+    if (!rc) rc = mdxrt_event_record(e0, s);
+    for (int i = 0; i < iters && !rc; i++) {
+        w.w = buf + per * (i % copies);
+        w.scale = (const float*)(buf + per * (i % copies) + wb);
+        rc = mdx_launch_gemv(dx, &w, 0, dy, s);
+    }
+    if (!rc) rc = mdxrt_event_record(e1, s);
+    if (!rc) rc = mdxrt_stream_sync(s);
+    float ms = 0.0f;
+    if (!rc) rc = mdxrt_event_elapsed_ms(e0, e1, &ms);
+    if (!rc) *avg_us = ms * 1000.0f / iters;
+    if (s) mdxrt_stream_sync(s);
+    mdxrt_free(buf);
+    mdxrt_free(dx);
+    mdxrt_free(dy);
+    mdxrt_event_destroy(e0);
+    mdxrt_event_destroy(e1);
+    mdxrt_stream_destroy(s);
+    return rc ? MATMUL_DECODER_ERR_RKNN : 0;
+}
+
 int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* scales,
                    const float* x, float* y) {
     if (kind < 0 || kind > 2 || M <= 0 || M > 64 || K <= 0 || N <= 0 || !w || !x || !y)

@@ -69,6 +69,11 @@ struct MatmulDecoderContext {
     int persist_head;        /* 1: that launch also runs the INT8 lm_head and the argmax */
     int persist_coop;        /* 1: launch it cooperatively (after an ordinary launch timed out) */
     unsigned spin_once;      /* test hook: spin limit of the next one-launch step (0: default) */
+    int poison_retry;        /* test hook: plant stale exchange words before the next retry */
+    int profile;             /* MDX_PROFILE=1: per-stage stats from device timestamps */
+    unsigned long long* d_trace;   /* [256][trace_ev] timestamps of the profiled step */
+    unsigned long long* h_trace;
+    int trace_ev;
     void* d_xbuf;            /* exchange words of the persistent step */
     mdx_persist_args pargs;
     mdx_state* h_state;
@@ -728,6 +733,19 @@ static pthread_mutex_t g_persist_mu = PTHREAD_MUTEX_INITIALIZER;
 static int persist_retry(MatmulDecoderContext* c) {
     if (!c->persist || c->persist_coop) return 0;
     c->persist_coop = 1;
+    if (c->poison_retry) {
+        c->poison_retry = 0;
+        if (mdx_persist_debug_poison(c->d_xbuf, c->L, c->stream)) return 0;
+    }
+    /* A workgroup of the timed-out launch that started late (crowded out by
+     * another grid) read the step counter after workgroup 0 had advanced it,
+     * and published words tagged with the epochs the retry would use.  Zeroing
+     * the exchange words, the counter with them, leaves no word the retry can
+     * accept before its own writer stores it (epoch 0 is never valid).  The
+     * stream is synchronised, so no workgroup of that launch is still running. */
+    if (mdxrt_fill_u32(c->d_xbuf, 0u, mdx_persist_xbuf_bytes() / 4, c->stream) ||
+        mdxrt_stream_sync(c->stream))
+        return 0;
     fprintf(stderr, "[MatmulDecoder] one-launch step timed out; retrying with cooperative launches\n");
     return 1;
 }
@@ -869,6 +887,16 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     if (mdxrt_host_alloc((void**)&c->h_samp, (MDX_SAMPLE_MAX_REPEAT + 64) * sizeof(int))) goto fail;
     memset(c->h_state, 0, sizeof(mdx_state));
     setup_persist(c);
+    {
+        const char* e = getenv("MDX_PROFILE");
+        c->profile = e && e[0] == '1';
+    }
+    if (c->profile && c->persist) {
+        c->trace_ev = mdx_persist_trace_events(c->L);
+        const size_t n = (size_t)256 * c->trace_ev;
+        c->h_trace = (unsigned long long*)malloc(n * 8);
+        if (!c->h_trace || mdxrt_malloc((void**)&c->d_trace, n * 8)) goto fail;
+    }
     if (md_verbose())
         printf("[MatmulDecoder] decode step: %s\n",
                c->persist ? (c->persist_head ? "one launch" : "layers in one launch, per-stage lm_head")
@@ -946,6 +974,8 @@ void matmul_decoder_destroy(MatmulDecoderContext* c) {
     mdxrt_graph_destroy(c->g_greedy);
     for (int i = 0; i < 4; i++) mdxrt_graph_destroy(c->pgraphs[i].exec);
     mdxrt_free(c->d_tokens);
+    mdxrt_free(c->d_trace);
+    free(c->h_trace);
     mdxrt_free(c->arena);
     mdxrt_host_free(c->h_state);
     mdxrt_host_free(c->h_io);
@@ -1000,6 +1030,72 @@ typedef struct {
     float u;
 } md_sample_req;
 
+/* ---- MDX_PROFILE=1: the stats breakdown of a one-launch step ----------- */
+
+static int cmp_u64(const void* a, const void* b) {
+    const unsigned long long x = *(const unsigned long long*)a, y = *(const unsigned long long*)b;
+    return x < y ? -1 : (x > y);
+}
+
+/* Median over the 256 workgroups of the time between events e0 and e1 of the
+ * traced step (100 MHz ticks). */
+static double seg_median(const MatmulDecoderContext* c, int e0, int e1, unsigned long long* tmp) {
+    int n = 0;
+    for (int b = 0; b < 256; b++) {
+        const unsigned long long* r = c->h_trace + (size_t)b * c->trace_ev;
+        if (r[e0] && r[e1]) tmp[n++] = r[e1] > r[e0] ? r[e1] - r[e0] : 0;
+    }
+    if (!n) return 0.0;
+    qsort(tmp, (size_t)n, sizeof *tmp, cmp_u64);
+    return (double)tmp[n / 2];
+}
+
+/* Splits the device time of a traced one-launch step over the reference's
+ * categories (src/matmul_decoder.c:1616-1623): matmul_ms the projection
+ * stages (with the norm / residual / SwiGLU they carry), cpu_ops_ms what
+ * cpu_ops.c does there (QK-norm, RoPE, the KV append, attention and the merge
+ * of its splits), lm_head_ms the lm_head with its argmax, rebind_ms the waits
+ * for other workgroups' results (the one-launch step's data movement between
+ * stages, where the reference rebinds B buffers).  Each category is the sum
+ * over layers of the per-segment medians over workgroups, scaled so that the
+ * four add up to the measured device time. */
+static void profile_split(MatmulDecoderContext* c, float dev_ms, int head, MatmulDecoderStats* st) {
+    static const int mm_seg[][2] = {{1, 2}, {6, 7}, {8, 9}, {9, 15}, {10, 11}};
+    static const int ops_seg[][2] = {{3, 12}, {12, 13}, {13, 4}};
+    static const int wait_seg[][2] = {{0, 1}, {2, 3}, {4, 5}, {5, 6}, {7, 8}, {15, 10}};
+    unsigned long long tmp[256];
+    double mm = 0, ops = 0, wait = 0, lm = 0;
+    for (int l = 0; l < c->L; l++) {
+        const int b = 16 * l;
+        for (size_t i = 0; i < sizeof mm_seg / sizeof mm_seg[0]; i++)
+            mm += seg_median(c, b + mm_seg[i][0], b + mm_seg[i][1], tmp);
+        for (size_t i = 0; i < sizeof ops_seg / sizeof ops_seg[0]; i++)
+            ops += seg_median(c, b + ops_seg[i][0], b + ops_seg[i][1], tmp);
+        for (size_t i = 0; i < sizeof wait_seg / sizeof wait_seg[0]; i++)
+            wait += seg_median(c, b + wait_seg[i][0], b + wait_seg[i][1], tmp);
+    }
+    if (head) {
+        const int e = 16 * c->L;
+        wait += seg_median(c, e - 16 + 11, e + 0, tmp);
+        lm += seg_median(c, e + 0, e + 1, tmp);
+        /* workgroup 0's reduction of the 256 keys */
+        const unsigned long long* r0 = c->h_trace;
+        if (r0[e + 2] > r0[e + 1]) lm += (double)(r0[e + 2] - r0[e + 1]);
+    }
+    const double sum = mm + ops + wait + lm;
+    const double k = sum > 0 ? (double)dev_ms / sum : 0.0;
+    st->matmul_ms = (float)(mm * k);
+    st->cpu_ops_ms = (float)(ops * k);
+    st->rebind_ms = (float)(wait * k);
+    st->lm_head_ms = (float)(lm * k);
+}
+
+static int trace_arm(MatmulDecoderContext* c) {
+    c->pargs.trace = c->d_trace;
+    c->pargs.trace_stride = c->trace_ev;
+    return mdxrt_fill_u32(c->d_trace, 0u, (size_t)256 * c->trace_ev * 2, c->stream);
+}
+
 static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding,
                    float* output_logits, int want_head, const md_sample_req* sr) {
     if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
@@ -1012,8 +1108,11 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
          * either; use head 0 like step_head(…, 0, …) */
         return matmul_decoder_step_head(c, token_id, embedding, 0, output_logits);
     }
+    const int prof = c->profile && c->persist && c->d_trace;
+    const int one_launch_head = c->persist && c->persist_head && want_head;
     if (c->persist) pthread_mutex_lock(&g_persist_mu);
     rc = set_state(c, token_id, embedding);
+    if (!rc && prof) rc = trace_arm(c);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
     if (c->persist && (c->persist_head || !want_head)) {
         if (!rc) rc = launch_persist(c, want_head, NULL);
@@ -1042,7 +1141,11 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
                                         c->stream);
     }
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
+    if (!rc && prof)
+        rc = mdxrt_d2h_async(c->h_trace, c->d_trace, (size_t)256 * c->trace_ev * 8, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    c->pargs.trace = NULL;
+    c->pargs.trace_stride = 0;
     if (c->persist) pthread_mutex_unlock(&g_persist_mu);
     if (rc) {
         fprintf(stderr, "[MatmulDecoder] step failed: %s\n", mdxrt_last_error());
@@ -1062,13 +1165,21 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     if (want_head) tok = c->h_state->argmax;
     if (sr) tok = c->h_samp[MDX_SAMPLE_MAX_REPEAT];
     const float total = (float)(md_now_ms() - t0);
+    /* Device times from events on the step's stream: layers_ms is the layers
+     * launch (with the lm_head too when it runs inside it), head_ms the
+     * separate head kernels.  Without MDX_PROFILE the one launch is not split:
+     * it all counts as matmul_ms. */
     c->stats.total_ms = total;
     c->stats.matmul_ms = layers_ms;
     c->stats.rebind_ms = 0.0f;
     c->stats.cpu_ops_ms = 0.0f;
-    /* 0 when the head runs inside the one launch (then it is in matmul_ms) */
-    c->stats.lm_head_ms = want_head ? head_ms : 0.0f;
-    c->stats.convert_ms = total - layers_ms - (want_head ? head_ms : 0.0f);
+    c->stats.lm_head_ms = want_head && !one_launch_head ? head_ms : 0.0f;
+    if (prof) {
+        profile_split(c, layers_ms, one_launch_head, &c->stats);
+        if (want_head && !one_launch_head) c->stats.lm_head_ms = head_ms;
+    }
+    c->stats.convert_ms = total - c->stats.matmul_ms - c->stats.cpu_ops_ms - c->stats.rebind_ms -
+                          c->stats.lm_head_ms;
     if (c->stats.convert_ms < 0) c->stats.convert_ms = 0;
     c->stats.n_steps++;
     return tok;
@@ -1375,6 +1486,7 @@ int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, f
     else if (!strcmp(which, "gate_up")) sel = 2;
     else if (!strcmp(which, "down")) sel = 3;
     else if (!strcmp(which, "lm_head")) sel = 4;
+    else if (!strcmp(which, "layer")) sel = 5;
     if (sel < 0 || (sel == 4 && c->n_lm > 1)) return MATMUL_DECODER_ERR_INVALID_ARG;
     const float eps = c->config.rms_eps;
     const mdx_wdesc* w0 = sel == 4 ? &c->lm : NULL;
@@ -1386,6 +1498,14 @@ int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, f
             case 1: rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream); break;
             case 2: rc = mdx_launch_norm_gemv(c->d_hidden, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream); break;
             case 3: rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream); break;
+            case 5:
+                /* the seven projections of one layer with their RMSNorms: merged
+                 * q|k|v, o (+residual), merged gate|up (+SwiGLU), down (+residual) */
+                rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_qkv, c->stream);
+                if (!rc) rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream);
+                if (!rc) rc = mdx_launch_norm_gemv(c->d_tmp, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream);
+                if (!rc) rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream);
+                break;
             default:
                 rc = mdx_launch_lmhead(c->d_hidden, c->d_final_norm, eps, w0, c->d_logits,
                                        c->d_partial, c->d_state, NULL, 0, c->stream);
@@ -1397,7 +1517,21 @@ int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, f
     float ms = 0.0f;
     mdxrt_event_elapsed_ms(c->ev0, c->ev1, &ms);
     if (avg_us) *avg_us = ms * 1000.0f / iters;
-    if (bytes) {
+    if (bytes && sel == 5) {
+        /* weights and scales of the four launches, the two norm vectors, and
+         * the activations each one reads and writes */
+        const md_layer* ly = &c->layers[0];
+        const mdx_wdesc* ws[4] = {&ly->qkv, &ly->o, &ly->gu, &ly->down};
+        double b = 0.0;
+        for (int i = 0; i < 4; i++)
+            b += (double)md_row_bytes(ws[i]->kind, ws[i]->K) * ws[i]->N + (ws[i]->scale ? 4.0 * ws[i]->N : 0.0);
+        b += 2.0 * 4.0 * c->d;                                   /* norm weights */
+        b += 4.0 * c->d + 4.0 * ly->qkv.N;                       /* qkv: hidden in, y out */
+        b += 2.0 * ly->o.K + 8.0 * c->d;                         /* o: fp16 in, read+write h */
+        b += 4.0 * c->d + 2.0 * ly->gu.N / 2;                    /* gate/up: h in, act out */
+        b += 2.0 * ly->down.K + 8.0 * c->d;                      /* down */
+        *bytes = b;
+    } else if (bytes) {
         const mdx_wdesc* w = sel == 4 ? &c->lm
                              : sel == 0 ? &c->layers[0].qkv
                              : sel == 1 ? &c->layers[0].o
@@ -1476,6 +1610,12 @@ int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* ou
     if (rc || c->h_state->pad[1]) return MATMUL_DECODER_ERR_RKNN;
     c->seq_len++;
     return ev;
+}
+
+int mdx_debug_persist_poison_retry(MatmulDecoderContext* c) {
+    if (!c || !c->persist) return MATMUL_DECODER_ERR_INVALID_ARG;
+    c->poison_retry = 1;
+    return 0;
 }
 
 int mdx_debug_persist_spin_limit(MatmulDecoderContext* c, unsigned rounds) {

@@ -11,6 +11,11 @@
  * last benchmark times 1.37.  Fixed on purpose: rmp_run writes a row-major
  * [M,N] fp32 output for every M (the reference's worker-major gather only
  * equals [M,N] when M == 1) and rmp_benchmark uses an fp32 output buffer.
+ *
+ * Any K is accepted, as in the reference: the kernels step K in blocks of
+ * 32, so a ragged K is zero-padded to Kp (zero weight rows, and input rows
+ * staged with zero tails in pinned memory); each padded term adds +0 to the
+ * fp32 sums.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -21,11 +26,13 @@
 
 struct RmpContext {
     RmpConfig config;
+    int Kp;                 /* K rounded up to a multiple of 32 */
     void* stream;
     uint8_t* d_w;
     uint16_t* d_x;
     float* d_y;
     float* d_scratch;
+    uint16_t* h_x;          /* pinned [M][Kp] staging when Kp != K (tails stay 0) */
     mdx_wdesc w;
     float last_benchmark_ms;
 };
@@ -39,10 +46,6 @@ RmpContext* rmp_create(const RmpConfig* config, const void* weights, const float
         fprintf(stderr, "rmp_create: N=%d must be divisible by n_workers=%d\n", config->N, n_workers);
         return NULL;
     }
-    if (config->K % 32 != 0) {
-        fprintf(stderr, "rmp_create: K=%d must be a multiple of 32\n", config->K);
-        return NULL;
-    }
     if (mdxrt_device_count() <= 0) {
         fprintf(stderr, "rmp_create: no GPU visible to the HIP runtime\n");
         return NULL;
@@ -52,18 +55,33 @@ RmpContext* rmp_create(const RmpConfig* config, const void* weights, const float
     c->config = *config;
     c->config.n_workers = n_workers;
     const int M = config->M, K = config->K, N = config->N;
+    const int Kp = (K + 31) / 32 * 32;
+    c->Kp = Kp;
     const int mchunk = M < 64 ? M : 64;
-    md_host_proj p = {0, K, N, (void*)weights, NULL};
-    uint8_t* rows = (uint8_t*)malloc((size_t)K * N * 2);
-    int rc = rows ? md_repack_rows(&p, MDX_W_F16, rows, NULL, 0) : -1;
+    /* [Kp,N] with zero rows k >= K, then the device row layout */
+    uint8_t* wpad = NULL;
+    const void* wsrc = weights;
+    if (Kp != K) {
+        wpad = (uint8_t*)calloc((size_t)Kp * N, 2);
+        if (wpad) memcpy(wpad, weights, (size_t)K * N * 2);
+        wsrc = wpad;
+    }
+    md_host_proj p = {0, Kp, N, (void*)wsrc, NULL};
+    uint8_t* rows = (uint8_t*)malloc((size_t)Kp * N * 2);
+    int rc = rows && wsrc ? md_repack_rows(&p, MDX_W_F16, rows, NULL, 0) : -1;
+    free(wpad);
     if (!rc) rc = mdxrt_stream_create(&c->stream);
-    if (!rc) rc = mdxrt_malloc((void**)&c->d_w, (size_t)K * N * 2);
-    if (!rc) rc = mdxrt_malloc((void**)&c->d_x, (size_t)M * K * 2);
+    if (!rc) rc = mdxrt_malloc((void**)&c->d_w, (size_t)Kp * N * 2);
+    if (!rc) rc = mdxrt_malloc((void**)&c->d_x, (size_t)M * Kp * 2);
     if (!rc) rc = mdxrt_malloc((void**)&c->d_y, (size_t)M * N * 4);
-    if (!rc) rc = mdxrt_malloc((void**)&c->d_scratch, mdx_gemm_scratch_floats(mchunk, N, K) * 4);
-    if (!rc) rc = mdxrt_fill_u32(c->d_scratch, 0u, mdx_gemm_scratch_floats(mchunk, N, K), c->stream);
+    if (!rc) rc = mdxrt_malloc((void**)&c->d_scratch, mdx_gemm_scratch_floats(mchunk, N, Kp) * 4);
+    if (!rc) rc = mdxrt_fill_u32(c->d_scratch, 0u, mdx_gemm_scratch_floats(mchunk, N, Kp), c->stream);
+    if (!rc && Kp != K) {
+        rc = mdxrt_host_alloc((void**)&c->h_x, (size_t)M * Kp * 2);
+        if (!rc) memset(c->h_x, 0, (size_t)M * Kp * 2);
+    }
     if (!rc) rc = mdxrt_stream_sync(c->stream);
-    if (!rc) rc = mdxrt_h2d(c->d_w, rows, (size_t)K * N * 2);
+    if (!rc) rc = mdxrt_h2d(c->d_w, rows, (size_t)Kp * N * 2);
     free(rows);
     if (rc) {
         fprintf(stderr, "rmp_create: %s\n", mdxrt_last_error());
@@ -73,21 +91,28 @@ RmpContext* rmp_create(const RmpConfig* config, const void* weights, const float
     c->w.w = c->d_w;
     c->w.scale = NULL;
     c->w.kind = MDX_W_F16;
-    c->w.K = K;
+    c->w.K = Kp;
     c->w.N = N;
     return c;
 }
 
 int rmp_run(RmpContext* c, const int16_t* input, float* output) {
     if (!c || !input || !output) return -1;
-    const int M = c->config.M, K = c->config.K, N = c->config.N;
-    int rc = mdxrt_h2d_async(c->d_x, input, (size_t)M * K * 2, c->stream);
+    const int M = c->config.M, K = c->config.K, N = c->config.N, Kp = c->Kp;
+    int rc;
+    if (Kp == K) {
+        rc = mdxrt_h2d_async(c->d_x, input, (size_t)M * K * 2, c->stream);
+    } else {
+        for (int m = 0; m < M; m++)
+            memcpy(c->h_x + (size_t)m * Kp, input + (size_t)m * K, (size_t)K * 2);
+        rc = mdxrt_h2d_async(c->d_x, c->h_x, (size_t)M * Kp * 2, c->stream);
+    }
     if (M == 1) {
         if (!rc) rc = mdx_launch_gemv_f16in(c->d_x, &c->w, c->d_y, c->stream);
     } else {
         for (int m0 = 0; m0 < M && !rc; m0 += 64) {
             const int mm = M - m0 < 64 ? M - m0 : 64;
-            rc = mdx_launch_gemm(c->d_x + (size_t)m0 * K, mm, &c->w, 0, c->d_y + (size_t)m0 * N,
+            rc = mdx_launch_gemm(c->d_x + (size_t)m0 * Kp, mm, &c->w, 0, c->d_y + (size_t)m0 * N,
                                  c->d_scratch, c->stream);
         }
     }
@@ -103,6 +128,7 @@ void rmp_destroy(RmpContext* c) {
     mdxrt_free(c->d_x);
     mdxrt_free(c->d_y);
     mdxrt_free(c->d_scratch);
+    mdxrt_host_free(c->h_x);
     mdxrt_stream_destroy(c->stream);
     free(c);
 }

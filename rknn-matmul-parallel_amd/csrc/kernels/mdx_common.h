@@ -115,6 +115,23 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Argmax key of logit v at index idx, reproducing argmax_f32
+// (src/cpu_ops.c:575-586: max starts at x[0], strict '>' over i = 1..n-1):
+// the largest key wins, equal values pick the lower index, -0 and +0 are
+// equal, a NaN never wins (key 0, which no number has) except at index 0,
+// where the reference's running maximum starts and no later '>' can replace
+// it, so it takes the largest key.
+__device__ __forceinline__ unsigned long long ref_argmax_key(float v, int idx) {
+    if (v != v) return idx == 0 ? ~0ull : 0ull;
+    unsigned u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
+}
+// The index a key was made from (0 for "no key").
+__device__ __forceinline__ int ref_argmax_index(unsigned long long k) {
+    return (k && k != ~0ull) ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+}
+
 // fp16 x fp16 products (exact in fp32) accumulated into fp32.
 __device__ __forceinline__ float dot8_f16(uint4 w, uint4 x, float acc) {
     acc = __builtin_amdgcn_fdot2(as_h2(w.x), as_h2(x.x), acc, false);

@@ -159,14 +159,6 @@ __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* 
     __syncthreads();
 }
 
-// Order-preserving key: larger value wins, equal values pick the lower index
-// (reference argmax: strict >, first index of the maximum).
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    unsigned u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
-}
-
 template <int KIND, int RW, int U>
 struct RowSet {
     int rows[RW];
@@ -276,8 +268,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         if (a.epi == EP_LOGITS) {
 #pragma unroll
             for (int r = 0; r < RW; r++) {
-                if (cur.valid[r] && y[r] == y[r]) {
-                    const unsigned long long k = argmax_key(y[r], cur.rows[r]);
+                if (cur.valid[r]) {
+                    const unsigned long long k = ref_argmax_key(y[r], cur.rows[r]);
                     if (k > best) best = k;
                 }
             }
@@ -301,7 +293,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             __threadfence();
             const unsigned long long k = atomicExch(a.amax_key, 0ull);
             atomicExch(a.done, 0u);
-            const int tok = k ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+            const int tok = ref_argmax_index(k);
             mdx_state* st = a.st;
             st->argmax = tok;
             st->token = tok;
@@ -361,10 +353,8 @@ __global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
         if ((lane % PER) == 0 && r < re) {
             const float y = tot * sc;
             a.out_f32[r] = y;
-            if (y == y) {
-                const unsigned long long k = argmax_key(y, r);
-                best = k > best ? k : best;
-            }
+            const unsigned long long k = ref_argmax_key(y, r);
+            best = k > best ? k : best;
         }
     };
     for (int base = first; base < re; base += 12 * U) {
@@ -427,7 +417,7 @@ __global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
         unsigned long long k = bkey[0];
         for (int w = 1; w < 4; w++) k = bkey[w] > k ? bkey[w] : k;
         *top = 0u;
-        const int tok = k ? (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull)) : 0;
+        const int tok = ref_argmax_index(k);
         mdx_state* st = a.st;
         st->argmax = tok;
         st->token = tok;

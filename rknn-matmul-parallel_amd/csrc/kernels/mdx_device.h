@@ -184,6 +184,10 @@ int mdx_persist_trace_events(int n_layers);
 /* One decode step (all layers, and the lm_head when head != 0).  A wait that
  * times out sets state->pad[1] = 1; the caller treats that as a failure. */
 int mdx_launch_persist_step(const mdx_persist_args* a, void* stream);
+/* Test hook: leaves hidden-state exchange words tagged with the epoch the next
+ * launch's first inter-layer wait accepts (stale data a late workgroup of a
+ * timed-out launch could have written). */
+int mdx_persist_debug_poison(void* xbuf, int n_layers, void* stream);
 
 /* ---- batch prefill (M <= 64) kernels ---- */
 

@@ -361,12 +361,6 @@ __device__ __forceinline__ void norm_to_x(const float (&h)[4], float4 w, float r
     reinterpret_cast<uint2*>(xs4)[t] = p;
 }
 
-__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
-    unsigned u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
-}
-
 // QK-norm (optional) + RoPE of one 128-wide head held in LDS, one wave.
 // With cache != NULL the results are rounded to fp16, stored there, and the
 // rounded values kept (the fp16 KV-cache semantic).
@@ -950,10 +944,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             if ((lane % PER) == 0 && r < re) {
                 const float y = tot * sc;
                 a.logits[r] = y;
-                if (y == y) {
-                    const unsigned long long k = argmax_key(y, r);
-                    best = k > best ? k : best;
-                }
+                const unsigned long long k = ref_argmax_key(y, r);
+                best = k > best ? k : best;
             }
         };
         // this wave's batches start at rb + wave*U, 4U rows apart
@@ -1017,7 +1009,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         if (t == 0) {
             unsigned long long kk = bkey[0];
             for (int w = 1; w < 4; w++) kk = bkey[w] > kk ? bkey[w] : kk;
-            const int res = kk ? (int)(0xFFFFFFFFu - (unsigned)(kk & 0xFFFFFFFFull)) : 0;
+            const int res = ref_argmax_index(kk);
             mdx_state* st = a.st;
             st->argmax = res;
             st->token = res;
@@ -1039,6 +1031,17 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
     }
     (void)ep_last;
+}
+
+// Test hook: words of the hidden-state region tagged with the epoch that the
+// next launch's layer-1 wait accepts (the step counter as it stands now),
+// holding 2.0 as payload: what a workgroup of a timed-out launch that started
+// late would have left behind.
+__global__ __launch_bounds__(256) void k_persist_poison(unsigned* xb, int L) {
+    const unsigned E = __hip_atomic_load(xb + W_CTRL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned ep = step_epoch(E, L, 0);
+    for (int i = threadIdx.x; i < NREP * 2 * D; i += 256)
+        __hip_atomic_store(xb + W_HD + i, 0x4000u | (ep << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 typedef void (*PersistKernel)(PArgs);
@@ -1076,6 +1079,13 @@ int mdx_persist_usable(int kind) {
         hipSuccess)
         return 0;
     return (long)per_cu * cus >= NB;
+}
+
+int mdx_persist_debug_poison(void* xbuf, int n_layers, void* stream) {
+    if (!xbuf || n_layers <= 0) return -1;
+    hipLaunchKernelGGL(k_persist_poison, dim3(1), dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<unsigned*>(xbuf), n_layers);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {

@@ -11,7 +11,10 @@
 //   2. v_i = logits_i / T when T != 1 (src/cpu_ops.c:597-601 divides).
 //   3. the k largest v, ties to the lower index: the reference's insertion
 //      (src/cpu_ops.c:604-624) takes an element only when it is strictly
-//      greater, so an equal value never displaces an earlier index.  Found by
+//      greater, so an equal value never displaces an earlier index.  Its k
+//      slots start as (index 0, -1e30) and only v > -1e30 displaces them, so
+//      NaN and values <= -1e30 never become candidates and missing slots stay
+//      (0, -1e30); the same rule holds here (such values get key 0).  Found by
 //      a radix select over an order-preserving 32-bit key (4 levels of 8
 //      bits; per-block LDS histograms summed in device memory), then the
 //      keys above the threshold are appended and the ties at it taken in
@@ -52,10 +55,14 @@ struct SampleScratch {
     float cand_val[kMaxK];
 };
 
+// The reference's empty-slot value: only v > kFloor can become a candidate.
+constexpr float kFloor = -1e30f;
+
 // Larger float -> larger key.  -0 and +0 share the key of +0 (they compare
-// equal as floats); NaN, which never compares greater, takes the lowest key.
+// equal as floats).  Values that can never be candidates (NaN, <= -1e30)
+// take key 0, which no candidate has.
 __device__ inline uint32_t order_key(float v) {
-    if (v != v) return 0u;
+    if (!(v > kFloor)) return 0u;
     const uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
@@ -180,14 +187,14 @@ __global__ __launch_bounds__(kBT) void k_sample_gather(const float* __restrict__
     for (int i = r0 + tid; i < r1; i += kBT) {
         const float v = tempered(logits[i], temp);
         const uint32_t key = order_key(v);
-        if (key > kstar) {
+        if (key > kstar) {   // kstar may be 0 (fewer than k candidates): key 0 never passes
             const int slot = atomicAdd(&sc->n_gt, 1);
             if (slot < kMaxK) {
                 sc->cand_idx[slot] = i;
                 sc->cand_val[slot] = v;
             }
         }
-        ties += key == kstar;
+        ties += key == kstar && kstar != 0u;
     }
     if (ties) atomicAdd(&s_ties, ties);
     __syncthreads();
@@ -233,8 +240,11 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
     }
     __syncthreads();
     const uint32_t kstar = s_kstar;
-    const int need = s_need;
-    const int greater = k - need;
+    // kstar == 0: fewer than k values can be candidates; every one of them is
+    // above the threshold and the other slots keep (index 0, -1e30)
+    const int need = kstar ? s_need : 0;
+    const int greater = k - s_need;
+    const int nc = greater + need;     // candidates that are real values
     if (tid < greater) {
         cidx[tid] = sc->cand_idx[tid];
         cval[tid] = sc->cand_val[tid];
@@ -265,20 +275,23 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
     __syncthreads();
 
     // rank by (value desc, index asc); the pairs are distinct, so the ranks
-    // are a permutation of 0..k-1
+    // are a permutation of 0..nc-1; the empty slots follow
     __shared__ uint32_t ckey[kMaxK];
-    if (tid < k) ckey[tid] = order_key(cval[tid]);
+    if (tid < nc) ckey[tid] = order_key(cval[tid]);
     __syncthreads();
-    if (tid < k) {
+    if (tid < nc) {
         const uint32_t kj = ckey[tid];
         const int ij = cidx[tid];
         int r = 0;
-        for (int m = 0; m < k; m++) {
+        for (int m = 0; m < nc; m++) {
             const uint32_t km = ckey[m];
             r += km > kj || (km == kj && cidx[m] < ij);
         }
         sidx[r] = ij;
         sval[r] = cval[tid];
+    } else if (tid < k) {
+        sidx[tid] = 0;
+        sval[tid] = kFloor;
     }
     __syncthreads();
 

@@ -126,6 +126,7 @@ def lib() -> C.CDLL:
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
             "mdx_decode_path": (C.c_int, [P]),
             "mdx_debug_persist_spin_limit": (C.c_int, [P, C.c_uint]),
+            "mdx_debug_persist_poison_retry": (C.c_int, [P]),
             "mdx_trace_step": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint64), C.c_int]),
             "mdx_kv_fill_normal": (C.c_int, [P, C.c_int, C.c_uint64]),
             "mdx_kv_read": (C.c_int, [P, C.c_int, C.c_int, C.c_int, _F, _F]),
@@ -133,6 +134,7 @@ def lib() -> C.CDLL:
             "mdx_generate_greedy": (C.c_int, [P, C.c_int, C.c_int, _I, _F]),
             "mdx_time_projection": (C.c_int, [P, C.c_char_p, C.c_int, _F, C.POINTER(C.c_double)]),
             "mdx_time_prefill": (C.c_int, [P, _F, C.c_int, C.c_int, _F]),
+            "mdx_time_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _F]),
             "mdx_debug_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
@@ -290,6 +292,13 @@ def qk_rope(nq, nkv, hd, pos, style, theta, eps, q_norm, k_norm, qkv):
     return q, k, v
 
 
+def time_gemv(kind: int, K: int, N: int, copies: int, iters: int) -> float:
+    """Average device microseconds of one GEMV launch over rotated weight copies."""
+    us = C.c_float(0.0)
+    _check(lib().mdx_time_gemv(kind, K, N, copies, iters, C.byref(us)), "time_gemv")
+    return float(us.value)
+
+
 def lmhead(kind: int, K: int, N: int, w_rows, scales, hidden, norm_w, eps: float):
     w = np.ascontiguousarray(w_rows)
     s, h, nw = _f32(scales), _f32(hidden), _f32(norm_w)
@@ -344,6 +353,10 @@ class Decoder:
     def path(self) -> int:
         """1: one launch per step; 0: per-stage kernels."""
         return lib().mdx_decode_path(self.h)
+
+    def poison_next_retry(self):
+        """Plant stale epoch-tagged exchange words before the next retry."""
+        _check(lib().mdx_debug_persist_poison_retry(self.h), "poison_retry")
 
     def force_spin_limit(self, rounds: int):
         """Next one-launch step gives up a wait after `rounds` polls (test hook)."""

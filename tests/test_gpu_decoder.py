@@ -304,10 +304,12 @@ def test_pybind_module_end_to_end(mdx, gpu, oracle_lib, models):
         dec.step_sample(1, 2.0)
 
 
-@pytest.mark.parametrize("M", [1, 5, 64, 70])
-def test_rmp_run_matches_oracle(mdx, gpu, oracle_lib, M):
+@pytest.mark.parametrize("M,K", [(1, 1024), (5, 1024), (64, 1024), (70, 1024),
+                                 # any K, as the reference accepts (zero-padded to 32)
+                                 (1, 100), (3, 1000), (67, 33), (1, 7)])
+def test_rmp_run_matches_oracle(mdx, gpu, oracle_lib, M, K):
     L = mdx.lib()
-    K, N = 1024, 1024
+    N = 1024
     rng = np.random.default_rng(M)
     w = (rng.standard_normal((K, N)) * 0.05).astype(np.float16)
     cfg = mdx.RmpConfig(M=M, K=K, N=N, type=0, layout=0, n_workers=2)

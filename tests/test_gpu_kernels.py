@@ -229,6 +229,49 @@ def test_lm_head_argmax_ties_pick_lowest_index(mdx, gpu, K, V, ties):
     assert tok == ties[0] and all(lg[i] == lg[ties[0]] for i in ties)
 
 
+@pytest.mark.parametrize("K,V", [(64, 4096), (1024, 16384)])
+def test_lm_head_argmax_signed_zero_and_nan(mdx, gpu, oracle_lib, K, V):
+    """The fused argmax follows argmax_f32 (src/cpu_ops.c:575-586) where a
+    sort key could differ: -0 and +0 tie (first index wins), a NaN at index 0
+    wins, a NaN elsewhere never does.  Logits are scale * dot with exact
+    integer dots, so the signs of the zeros are the scales' signs."""
+    h = np.zeros(K, np.float32)
+    h[0] = 1.0                                         # x16[0] = fp16(sqrt(K)), the rest 0
+    q = np.zeros((V, K), np.int8)
+    q[:, 0] = 1
+    far = V - 5                                        # another block of the streaming kernel
+    zero_rows = [0, 1, 2, far]
+    q[zero_rows, 0] = 0
+
+    def run(s):
+        tok, lg = mdx.lmhead(1, K, V, q, s, h, np.ones(K, np.float32), 1e-6)
+        return tok, lg
+
+    # every other row is negative; rows 0, 1 are -0.0, rows 2 and far +0.0
+    s = -np.ones(V, np.float32)
+    s[[2, far]] = 1.0
+    tok, lg = run(s)
+    assert np.signbit(lg[0]) and not np.signbit(lg[2]) and lg[2] == 0.0
+    assert tok == oracle_lib.argmax(lg) == 0
+    # a +0 first, then -0 rows: still the first
+    s = -np.ones(V, np.float32)
+    s[1] = 1.0
+    tok, lg = run(s)
+    assert tok == oracle_lib.argmax(lg) == 0
+    # NaN at index 0 wins over a larger value later
+    s = -np.ones(V, np.float32)
+    s[0] = np.nan
+    s[far - 10] = 2.0
+    tok, lg = run(s)
+    assert np.isnan(lg[0]) and tok == oracle_lib.argmax(lg) == 0
+    # NaN elsewhere is skipped
+    s = -np.ones(V, np.float32)
+    s[[5, far - 10]] = np.nan
+    s[700] = 3.0
+    tok, lg = run(s)
+    assert tok == oracle_lib.argmax(lg) == 700
+
+
 def test_lm_head_fp32_and_fp16_rows(mdx, gpu, oracle_lib):
     rng = np.random.default_rng(11)
     K, V = 1024, 2048

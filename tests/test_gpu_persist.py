@@ -249,6 +249,62 @@ def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models,
         assert t == t_ref and np.array_equal(lg, l_ref)
 
 
+def test_retry_ignores_stale_exchange_words(mdx, gpu, oracle_lib, models, capfd):
+    """A timed-out launch whose late workgroups left words tagged with the
+    epochs the retry would use (planted by a test hook between the failed
+    launch and the retry): the retry clears the exchange words first, so its
+    result still equals an undisturbed context's."""
+    cfg, get = models
+    path = get(1)
+    g_ref, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    g, _ = _pair(mdx, oracle_lib, cfg, path, 1)
+    for d in (g_ref, g):
+        d.kv_fill_normal(150, 17)
+    t_ref, l_ref = g_ref.step(555)
+    g.force_spin_limit(1)
+    g.poison_next_retry()
+    t, lg = g.step(555)
+    assert "retrying with cooperative launches" in capfd.readouterr().err
+    assert t == t_ref and np.array_equal(lg, l_ref)
+    t_ref, l_ref = g_ref.step(t_ref)
+    t, lg = g.step(t)
+    assert t == t_ref and np.array_equal(lg, l_ref)
+
+
+def test_stats_breakdown_with_profile(mdx, gpu, oracle_lib, models, monkeypatch):
+    """MatmulDecoderStats (src/matmul_decoder.c:1616-1623): without
+    MDX_PROFILE the one launch counts as matmul_ms; with MDX_PROFILE=1 it is
+    split over matmul / cpu_ops / rebind (waits) / lm_head from the step's
+    own timestamps.  Every field is >= 0 and the parts add up to total_ms;
+    prefill-mode steps report no lm_head time.  The profiled step computes
+    the same logits."""
+    cfg, get = models
+    path = get(0)
+    plain, _ = _pair(mdx, oracle_lib, cfg, path, 0)
+    monkeypatch.setenv("MDX_PROFILE", "1")
+    prof, _ = _pair(mdx, oracle_lib, cfg, path, 0)
+    monkeypatch.delenv("MDX_PROFILE")
+    for d in (plain, prof):
+        d.kv_fill_normal(300, 21)
+    fields = ("matmul_ms", "rebind_ms", "convert_ms", "cpu_ops_ms", "lm_head_ms")
+    for i, tok in enumerate((12, 3456, 78)):
+        t0, l0 = plain.step(tok)
+        t1, l1 = prof.step(tok)
+        assert t0 == t1 and np.array_equal(l0, l1)
+        a, b = plain.stats(), prof.stats()
+        for st in (a, b):
+            assert st["n_steps"] == i + 1 and st["total_ms"] > 0
+            assert all(st[f] >= 0 for f in fields), st
+            parts = sum(st[f] for f in fields)
+            assert abs(parts - st["total_ms"]) <= 1e-3 + 1e-4 * st["total_ms"], st
+        assert a["cpu_ops_ms"] == a["rebind_ms"] == a["lm_head_ms"] == 0 and a["matmul_ms"] > 0
+        assert min(b["matmul_ms"], b["cpu_ops_ms"], b["rebind_ms"], b["lm_head_ms"]) > 0, b
+    # prefill mode: no logits, no lm_head
+    assert prof.step(5, logits=False)[0] == 0
+    st = prof.stats()
+    assert st["lm_head_ms"] == 0 and st["matmul_ms"] > 0 and st["n_steps"] == 4
+
+
 def test_two_contexts_in_two_threads(mdx, gpu, oracle_lib, models, capfd):
     """Two contexts stepping at the same time from two threads: their one-launch
     steps are serialised inside the library, so neither grid is crowded out

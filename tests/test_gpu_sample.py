@@ -134,3 +134,30 @@ def test_step_sample_through_the_decoder(mdx, gpu, oracle_lib, workdir):
     assert a.seq_len == b.seq_len == 12
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("k", [1, 8, 300])
+def test_top_k_floor_and_nan_as_the_reference(mdx, gpu, oracle_lib, k):
+    """Only values above -1e30 become candidates (the reference's slots start
+    at (0, -1e30) and take a value only when it is strictly greater; NaN
+    never is); missing slots stay (0, -1e30).  Checked bit-exact against the
+    oracle with -inf, -1e30, NaN and, in the last case, fewer real values
+    than k."""
+    V = 5000
+    x = _logits(V, 900 + k)
+    x[[3, 17, 4000]] = -np.inf
+    x[[5, 4001]] = np.nan
+    x[[9, 2500]] = -1e30
+    x[[11]] = -2e30
+    for u in (0.0, 0.5, 0.999):
+        _check(mdx, oracle_lib, x, top_k=k, u=u)
+    y = np.full(V, -np.inf, np.float32)
+    y[[7, 70, 700]] = [1.0, 2.0, -3.0]
+    y[[8, 80]] = np.nan
+    y[90] = -1e30
+    for u in (0.0, 0.4, 0.999):
+        _check(mdx, oracle_lib, y, top_k=k, u=u)
+    z = np.full(V, np.nan, np.float32)
+    z[[10, 20]] = -np.inf
+    tok = _check(mdx, oracle_lib, z, top_k=k, u=0.3)
+    assert tok == 0

@@ -221,6 +221,33 @@ def test_argmax_first_index_wins(oracle_lib):
     assert oracle_lib.argmax(np.full(100, -2.0, np.float32)) == 0
 
 
+def _argmax_strict(x):
+    """argmax_f32 (src/cpu_ops.c:575-586) as written: the running maximum
+    starts at x[0] and moves only on a strict '>'."""
+    mv, mi = x[0], 0
+    for i in range(1, len(x)):
+        if x[i] > mv:
+            mv, mi = x[i], i
+    return mi
+
+
+def test_argmax_signed_zero_and_nan(oracle_lib):
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    cases = [
+        [-0.0, 0.0, -1.0],          # -0 and +0 are equal: the first index
+        [0.0, -0.0, -3.0],
+        [-5.0, -0.0, 0.0, -0.0],
+        [nan, 3.0, 7.0],            # NaN at 0: no later value compares greater
+        [1.0, nan, 2.0, nan],       # NaN elsewhere never wins
+        [-inf, nan, nan],
+        [nan, nan],
+        [-inf, -inf, -1e30],
+    ]
+    for c in cases:
+        x = np.array(c, np.float32)
+        assert oracle_lib.argmax(x) == _argmax_strict(x), c
+
+
 # ---- projections ---------------------------------------------------------------------
 
 def test_matmul_f16_float64(oracle_lib):
