@@ -15,9 +15,16 @@ Also reported: the roofline of that kernel (algorithmic bytes of a step over
 its average duration, HIP events on the decoder's stream), with the HBM
 traffic measured by rocprofv3 counters when its summary is present under
 profiles/; the per-stage kernels of the general path (the fallback for other
-shapes); the M=60 INT8 batch prefill (28 layers, 60 tokens from an empty
-cache); and the oracle (the scalar C restatement of the reference CPU path)
-timed on this host on a bounded sample of the same decode workload.
+shapes); and the oracle (the scalar C restatement of the reference CPU path)
+timed on this host on a bounded sample of the same decode workload.  The
+other workloads of the metric each get their own object under "configs":
+  1  one INT8 GEMV tile 1 x 1024 x 4096 with per-column scales, 1024
+     back-to-back launches over 128 rotated weight copies (541 MB);
+  2  one fp16 layer's seven projections with their RMSNorms at M = 1 (four
+     launches), cycling through the 28 layers of the decode model;
+  4  the M=60 INT8 batch prefill (28 layers, 60 tokens from an empty cache);
+  5  W4A16 greedy decode at KV 4096 -> 4224 (128 steps), int4 layer weights
+     with fp16 scales, INT8 lm_head.
 
 Usage: python bench.py [--gpus 1] [--steps 64] [--warmup 8]
 """
@@ -118,6 +125,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of oracle decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-w4", action="store_true", help="skip the W4A16 KV 4096 decode (config 5)")
     ap.add_argument("--workload", default="fp16_kv512", choices=["fp16_kv512", "w4a16_kv4096"],
                     help="decode workload: fp16 layers at KV 512 (the default line), or W4A16 at "
                          "KV 4096 (decode only)")
@@ -199,6 +207,10 @@ def main() -> int:
         us, b = dec.time_projection(name, iters)
         kernels[name] = {"avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
                          "per_step_us": round(us * per_step, 1)}
+    layer_us = layer_bytes = None
+    if not args.probe and not w4:
+        dec.time_projection("layer", 28)
+        layer_us, layer_bytes = dec.time_projection("layer", 280)
     path_kind = dec.path
     dec.close()
     step_us = dev_ms * 1000.0 / args.steps
@@ -207,6 +219,26 @@ def main() -> int:
     if os.path.exists(tfile) and not w4:
         with open(tfile) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    configs = {}
+    if not args.probe and not w4:
+        # ---- config 2: one fp16 layer's projections at M=1 (per-stage kernels) ----
+        us, b = layer_us, layer_bytes
+        configs["2_fp16_layer_projections_m1"] = {
+            "avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
+            "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+            "kernels": "k_gemv: RMSNorm+q|k|v, o+residual, RMSNorm+gate|up+SwiGLU, down+residual",
+            "rotation": "28 layers' distinct weights (881 MB)"}
+        log(f"config 2 layer projections: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
+        # ---- config 1: the INT8 lm_head tile GEMV 1 x 1024 x 4096 ----
+        us1 = mdx.time_gemv(1, 1024, 4096, 128, 1024)
+        b1 = 1024 * 4096 + 4.0 * 4096 + 4.0 * 1024 + 4.0 * 4096
+        configs["1_int8_tile_gemv_1x1024x4096"] = {
+            "avg_us": round(us1, 3), "bytes": b1, "GBps": round(b1 / us1 / 1e3, 1),
+            "hbm_frac": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4),
+            "kernels": "k_gemv<int8> (fp32 x rounded to fp16, per-column scales)",
+            "rotation": "1024 launches over 128 weight copies (541 MB)"}
+        log(f"config 1 int8 tile GEMV: {us1:.2f} us, {b1 / us1 / 1e3:.0f} GB/s")
 
     # ---- batch prefill M=60 through 28 INT8 layers ----
     prefill = None
@@ -225,6 +257,35 @@ def main() -> int:
                    "mfma_frac_layers": round(flops / (pms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
                    "note": "28 INT8 layers, causal GQA over 60 positions, device time (HIP events)"}
         log(f"prefill M=60: {pms:.3f} ms")
+
+    if prefill:
+        configs["4_prefill_m60_int8"] = prefill
+
+    # ---- config 5: W4A16 greedy decode at KV 4096 (128 steps) ----
+    if not args.probe and not w4 and not args.no_w4:
+        d5 = dict(d, max_seq_len=4224)
+        cfg5 = mdx.qwen3_0_6b_config(name="qwen3-0.6b-synthetic-w4", **d5)
+        path4 = model_dir(mdx, "decode_int4_seed1005", cfg5, 2, 1005)
+        n5, w5 = 128, 8
+        dec4 = mdx.Decoder(path4, cfg5, "int4", 4096 + n5 + w5)
+        dec4.kv_fill_normal(4096, 1005)
+        dec4.generate_greedy(START_TOKEN, w5)
+        dec4.kv_fill_normal(4096, 1005)
+        t0 = time.perf_counter()
+        toks5, dev5 = dec4.generate_greedy(START_TOKEN, n5)
+        wall5 = time.perf_counter() - t0
+        dec4.close()
+        b5 = step_bytes(d5, list(range(4096, 4096 + n5)), 2)
+        us5 = dev5 * 1000.0 / n5
+        configs["5_w4a16_decode_kv4096"] = {
+            "ms_per_token": round(wall5 * 1000.0 / n5, 5), "tokens_per_s": round(n5 / wall5, 2),
+            "steps": n5, "kv": f"4096->{4096 + n5}",
+            "roofline": {"bound": "hbm", "kernel": "k_persist_step<i4>", "avg_us": round(us5, 2),
+                         "bytes_per_launch": b5, "achieved": round(b5 / (us5 * 1e-6) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(b5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "tokens_head": toks5[:8]}
+        log(f"config 5 W4A16 KV 4096: {wall5 * 1000.0 / n5 * 1000:.1f} us/token wall, {us5:.1f} us device")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -257,11 +318,16 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(bytes_step / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
+                     "traffic_source": ("profiles/k_persist_step_fp16_decode_kv512_traffic.json: "
+                                        "rocprofv3 FETCH_SIZE and WRITE_SIZE passes over the same "
+                                        "kernel at KV 512..520, scaled by a copy kernel's counts "
+                                        "(not this run)") if traffic else None,
                      "bytes_per_launch": bytes_step, "avg_us": round(step_us, 2)},
         "wall_roofline_frac": round(bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "api_step_ms": api_ms,
         "per_stage_path_kernels": kernels,
         "prefill_m60": prefill,
+        "configs": configs,
         "cpu_baseline": cpu,
         "tokens_head": toks[:8],
     }
