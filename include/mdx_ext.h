@@ -179,6 +179,30 @@ int mdx_debug_sample(const float* logits, int V, const SamplingParams* params, f
 int matmul_decoder_step_sample(MatmulDecoderContext* ctx, int token_id, const float* embedding,
                                const SamplingParams* params, float uniform, float* output_logits);
 
+/* No counterpart in the reference: the device sampler for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  A variant of mdx_debug_sample without the repetition
+ * penalty that takes device pointers: logits[V] (read only), out[2] (token,
+ * candidates kept after top-p), top_idx/top_val[top_k] (may be NULL); k =
+ * top_k must be in [1, min(V, MDX_SAMPLE_MAX_TOP_K)] (larger k is rejected
+ * with a message: the scratch holds 1024 candidates).  Enqueued on `stream`
+ * (NULL: the default stream); returns without synchronising.  It calls no
+ * allocator: its 13 KB of scratch is a static device array of the library,
+ * one per GPU, held until the process ends.  Calls that overlap on one GPU
+ * share that scratch and race; serialise them.  Returns 0, -1 for bad
+ * arguments, -4 on a HIP failure. */
+int mdx_sample_topk_noalloc(const float* logits, int V, float temperature, int top_k, float top_p,
+                            float uniform, int* out, int* top_idx, float* top_val, void* stream);
+
+/* Device memory and synchronous copies on the current device, for callers
+ * and tests that hand device pointers to the device-pointer entry points.
+ * Return 0 or a negative error. */
+int mdx_device_malloc(void** ptr, size_t bytes);
+int mdx_device_free(void* ptr);
+int mdx_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mdx_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mdx_device_synchronize(void);
+
 /* ---- host helpers shared with tools (no GPU needed) ---- */
 
 /* INT8 lm_head quantiser of the reference (per vocab row of the fp16 copy):

@@ -387,3 +387,22 @@ int mdx_debug_sample(const float* logits, int V, const SamplingParams* params, f
     free(toks);
     return scope_close(&s, rc);
 }
+
+int mdx_device_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return MATMUL_DECODER_ERR_INVALID_ARG;
+    return mdxrt_malloc(ptr, bytes) ? MATMUL_DECODER_ERR_MEMORY : 0;
+}
+
+int mdx_device_free(void* ptr) { return mdxrt_free(ptr) ? MATMUL_DECODER_ERR_RKNN : 0; }
+
+int mdx_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (!dst || !src) return MATMUL_DECODER_ERR_INVALID_ARG;
+    return mdxrt_h2d(dst, src, bytes) ? MATMUL_DECODER_ERR_RKNN : 0;
+}
+
+int mdx_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (!dst || !src) return MATMUL_DECODER_ERR_INVALID_ARG;
+    return mdxrt_d2h(dst, src, bytes) ? MATMUL_DECODER_ERR_RKNN : 0;
+}
+
+int mdx_device_synchronize(void) { return mdxrt_device_sync() ? MATMUL_DECODER_ERR_RKNN : 0; }

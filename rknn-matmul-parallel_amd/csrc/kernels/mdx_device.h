@@ -56,6 +56,7 @@ int mdxrt_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
 int mdxrt_stream_create(void** stream);
 int mdxrt_stream_destroy(void* stream);
 int mdxrt_stream_sync(void* stream);
+int mdxrt_device_sync(void);
 int mdxrt_graph_begin(void* stream);
 int mdxrt_graph_end(void* stream, void** exec);
 int mdxrt_graph_launch(void* exec, void* stream);

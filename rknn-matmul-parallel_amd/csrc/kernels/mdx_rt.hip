@@ -111,6 +111,11 @@ int mdxrt_stream_sync(void* stream) {
     return 0;
 }
 
+int mdxrt_device_sync(void) {
+    MDX_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return 0;
+}
+
 int mdxrt_graph_begin(void* stream) {
     MDX_CHECK(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
               "hipStreamBeginCapture");

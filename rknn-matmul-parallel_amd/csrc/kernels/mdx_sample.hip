@@ -33,6 +33,8 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <mutex>
 
 #include "mdx_device.h"
 
@@ -332,11 +334,57 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
     if (top_val && tid < k) top_val[tid] = sval[tid];
 }
 
+// The sampler scratch of mdx_sample_topk_noalloc, for callers that cannot
+// allocate: one copy per device, held until the process ends.  Host code
+// never passes the name itself to a kernel (on the host it is only a handle);
+// it uses the device address hipGetSymbolAddress returns for the current
+// device, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[sizeof(SampleScratch)];
+constexpr int kMaxDevices = 64;
+void* g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of this device's scratch, or nullptr (with a message).
+void* noalloc_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fprintf(stderr, "mdx_sample_topk_noalloc: no usable current device (%d)\n", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "mdx_sample_topk_noalloc: hipGetSymbolAddress: %s\n", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_addr[dev] = p;
+    }
+    return g_scratch_addr[dev];
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t mdx_sample_scratch_bytes(void) { return sizeof(SampleScratch); }
+
+int mdx_sample_topk_noalloc(const float* logits, int V, float temperature, int top_k, float top_p,
+                            float uniform, int* out, int* top_idx, float* top_val, void* stream) {
+    if (top_k > kMaxK) {
+        fprintf(stderr, "mdx_sample_topk_noalloc: top_k=%d exceeds the scratch capacity of %d candidates\n",
+                top_k, kMaxK);
+        return -1;
+    }
+    if (!logits || V <= 0 || top_k < 1 || top_k > V || !(temperature > 0.0f) || !(uniform >= 0.0f) ||
+        !(uniform <= 1.0f) || !out)
+        return -1;
+    void* sc = noalloc_scratch();
+    if (!sc) return -4;
+    return mdx_launch_topk_sample(logits, V, temperature, top_k, top_p, uniform, sc, out, top_idx, top_val,
+                                  stream);
+}
 
 int mdx_launch_repeat_penalty(float* logits, const int* tokens, int n, float penalty, void* stream) {
     if (n <= 0) return 0;

@@ -135,6 +135,13 @@ def lib() -> C.CDLL:
             "mdx_time_projection": (C.c_int, [P, C.c_char_p, C.c_int, _F, C.POINTER(C.c_double)]),
             "mdx_time_prefill": (C.c_int, [P, _F, C.c_int, C.c_int, _F]),
             "mdx_time_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _F]),
+            "mdx_sample_topk_noalloc": (C.c_int, [P, C.c_int, C.c_float, C.c_int, C.c_float, C.c_float,
+                                                  P, P, P, P]),
+            "mdx_device_malloc": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t]),
+            "mdx_device_free": (C.c_int, [P]),
+            "mdx_memcpy_h2d": (C.c_int, [P, P, C.c_size_t]),
+            "mdx_memcpy_d2h": (C.c_int, [P, P, C.c_size_t]),
+            "mdx_device_synchronize": (C.c_int, []),
             "mdx_debug_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
