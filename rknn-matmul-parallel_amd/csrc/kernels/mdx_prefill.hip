@@ -1,8 +1,10 @@
 // mdx_prefill.hip — batch prefill (M <= 64 rows) kernels for gfx950.
 //
 // Projections (reference: src/matmul_decoder.c:1841-1899, run_batch_matmul)
-// run on MFMA v_mfma_f32_16x16x32_f16, one block per 64 x 32 output tile with
-// the K range split over its waves (see k_gemm).
+// run on MFMA v_mfma_f32_16x16x32_f16: the qkv and gate/up projections one
+// block per 64 x 32 output tile with the K range split over its waves
+// (k_gemm), the o and down projections split over blocks along K with the
+// activation panel staged in LDS (k_gemm_s).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -13,6 +15,8 @@
 using namespace mdx;
 
 namespace {
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxM = 64;
 constexpr int kNT = 32;        // weight rows (output columns) per block
@@ -283,6 +287,101 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm(const uint1
             float* dst = out_f32 + (size_t)row * N + n;
             store_wt(dst, epi == 1 ? *dst + y : y);
         }
+    }
+}
+
+// ---- projections, split-K over blocks: k_gemm_s -------------------------------
+//
+// The o and down projections (K a multiple of kKS, K / kKS <= kMaxSplits
+// splits).  Block (tile, split) stages the activation panel X[64][kKS] of its
+// split in LDS once (all 16-byte loads issued together), then each of its NW
+// waves owns 16 output columns (weight rows) over the whole panel: no
+// cross-wave reduction.  The weights of a wave are requested before the
+// panel, so their HBM latency overlaps the staging.  The raw fp32 sums go to
+// part[split][row][N] for k_residual_norm (which sums the splits in split
+// order and applies the column scales), written as whole 256-byte row
+// segments through LDS with 16-byte device-scope stores: in a standalone
+// timeline of this kernel, 4-byte device-scope stores of the MFMA fragments
+// took ~4 us per launch, these ~0.5 us.
+constexpr int kKS = 256;
+
+template <int KIND, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemm_s(const uint16_t* __restrict__ x16, int M, int K,
+                                                    const uint8_t* __restrict__ w, int N, float* part) {
+    using GK = GemmKind<KIND>;
+    constexpr int EPL = GK::EPL;               // k per 16-byte weight load
+    constexpr int CK = 4 * EPL;                // k per chunk (4 lane groups)
+    constexpr int NCH = kKS / CK;              // chunks per split
+    constexpr int STEPS = EPL / 8;             // MFMA k-steps per chunk
+    constexpr int RS = kKS / 8 + 1;            // uint4 per LDS panel row (16-byte pad)
+    constexpr int OW = 16 * NW + 4;            // floats per LDS output row
+    static_assert(kMaxM * RS * 16 >= kMaxM * OW * 4, "output tile fits the panel");
+    __shared__ uint4 xs4[kMaxM * RS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int tile = blockIdx.x, split = blockIdx.y;
+    const int k0 = split * kKS;
+    const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
+    const int wrow = (tile * NW + wave) * 16 + c16;      // this lane's weight row
+    uint4 wv[NCH];
+    {
+        const uint8_t* wr = w + (size_t)wrow * row_bytes + (size_t)(k0 + g * EPL) * 16 / EPL;
+#pragma unroll
+        for (int j = 0; j < NCH; j++) wv[j] = *reinterpret_cast<const uint4*>(wr + (size_t)j * CK * 16 / EPL);
+    }
+    // the panel: 64 rows (rows >= M repeat row M-1) x kKS fp16
+    {
+        constexpr int CHUNKS = kMaxM * (kKS / 8);
+        constexpr int PER = CHUNKS / (NW * 64);
+        static_assert(CHUNKS % (NW * 64) == 0, "panel split");
+        uint4 v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = tid + i * NW * 64;
+            const int row = c / (kKS / 8), col = c % (kKS / 8);
+            const int rr = row < M ? row : M - 1;
+            v[i] = *reinterpret_cast<const uint4*>(x16 + (size_t)rr * K + k0 + 8 * col);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = tid + i * NW * 64;
+            xs4[(c / (kKS / 8)) * RS + c % (kKS / 8)] = v[i];
+        }
+    }
+    __syncthreads();
+    float4_t acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        half8_t b[STEPS];
+        widen_b<KIND>(wv[j], b);
+#pragma unroll
+        for (int s = 0; s < STEPS; s++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // A fragment: row 16r + c16, k = j*CK + g*EPL + 8s .. +7
+                const half8_t a = __builtin_bit_cast(half8_t, xs4[(16 * r + c16) * RS + (j * CK + g * EPL) / 8 + s]);
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[s], acc[r], 0, 0, 0);
+            }
+    }
+    __syncthreads();   // the panel is reused for the output tile
+    float* ot = reinterpret_cast<float*>(xs4);
+    // D fragment: lane holds column c16 of this wave's 16, rows 16r + 4g + i
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) ot[(16 * r + 4 * g + i) * OW + 16 * wave + c16] = acc[r][i];
+    __syncthreads();
+    constexpr int F4 = 4 * NW;                 // float4 per output row
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(part, (short)0, 0x7fffffff, 0x00020000);
+    for (int idx = tid; idx < kMaxM * F4; idx += NW * 64) {
+        const int row = idx / F4, c4 = idx % F4;
+        if (row >= M) continue;
+        const float4 v = *reinterpret_cast<const float4*>(ot + row * OW + 4 * c4);
+        const size_t off = (((size_t)split * kMaxM + row) * N + (size_t)tile * 16 * NW + 4 * c4) * 4;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, (unsigned)off, 0, 16);
     }
 }
 
@@ -594,6 +693,32 @@ __global__ void k_copy_row(const float* x, int row, int d, float* dst) {
 
 }  // namespace
 
+// k_gemm_s serves the shape: K a multiple of kKS with at most kMaxSplits
+// splits, N a multiple of the 64 columns of a block (4 waves).
+static bool gemm_s_ok(int M, const mdx_wdesc* w) {
+    return M > 0 && M <= kMaxM && w->K % kKS == 0 && w->K / kKS <= kMaxSplits && w->N % 64 == 0;
+}
+
+static int gemm_s_launch(const uint16_t* x16, int M, const mdx_wdesc* w, float* part, void* stream) {
+    dim3 grid(w->N / 64, w->K / kKS);
+    const uint8_t* wp = (const uint8_t*)w->w;
+    hipStream_t s = (hipStream_t)stream;
+    switch (w->kind) {
+        case MDX_W_F16:
+            hipLaunchKernelGGL((k_gemm_s<MDX_W_F16, 4>), grid, dim3(256), 0, s, x16, M, w->K, wp, w->N, part);
+            break;
+        case MDX_W_I8:
+            hipLaunchKernelGGL((k_gemm_s<MDX_W_I8, 4>), grid, dim3(256), 0, s, x16, M, w->K, wp, w->N, part);
+            break;
+        case MDX_W_I4:
+            hipLaunchKernelGGL((k_gemm_s<MDX_W_I4, 4>), grid, dim3(256), 0, s, x16, M, w->K, wp, w->N, part);
+            break;
+        default:
+            return -5;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 extern "C" {
 
 int mdx_launch_rmsnorm_rows(const float* x, const float* w, float eps, int M, int d,
@@ -628,8 +753,12 @@ static int residual_splits(int N, int K) {
 
 size_t mdx_gemm_scratch_floats(int M, int N, int K) {
     (void)M;
-    return (size_t)residual_splits(N, K) * kMaxM * N;
+    const size_t a = (size_t)residual_splits(N, K) * kMaxM * N;
+    const size_t b = K % kKS == 0 ? (size_t)(K / kKS) * kMaxM * N : 0;
+    return a > b ? a : b;
 }
+
+
 
 static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
                        float* part, int ns, void* stream) {
@@ -669,13 +798,18 @@ int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue
     (void)scratch;
     return gemm_launch(x16, M, w, epilogue, out, nullptr, 1, stream);
 }
-
 int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w, float* hidden,
                                   const float* norm_w, float eps, uint16_t* x16_out, float* scratch,
                                   void* stream) {
     if (w->N % 4) return -1;   // float4 rows in k_residual_norm
-    const int ns = residual_splits(w->N, w->K);
-    int rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
+    int ns, rc;
+    if (gemm_s_ok(M, w)) {
+        ns = w->K / kKS;
+        rc = gemm_s_launch(x16, M, w, scratch, stream);
+    } else {
+        ns = residual_splits(w->N, w->K);
+        rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
+    }
     if (rc) return rc;
     const int R = w->N % 1024 == 0 ? w->N / 1024 : 0;
     auto kern = R == 1 ? k_residual_norm<1> : R == 2 ? k_residual_norm<2> : R == 4 ? k_residual_norm<4>

@@ -224,6 +224,36 @@ def test_create_destroy_cycles_release_device_memory(mdx, gpu, oracle_lib, model
     assert before - after < (64 << 20)
 
 
+@pytest.mark.parametrize("quant", [0, 1, 2])
+@pytest.mark.parametrize("M", [60, 64, 17, 1])
+def test_prefill_full_width_matches_oracle(mdx, gpu, oracle_lib, models, quant, M):
+    """Batch prefill on the 0.6B layer shape (the split-K MFMA projections
+    with the SwiGLU finished by the last split, the RoPE/append and residual
+    kernels summing the splits): K/V rows of both layers and the lm_head on
+    the last row against the oracle, then a second chunk on top of a
+    non-empty cache."""
+    cfg, get = models
+    g, o = _pair(mdx, oracle_lib, cfg, get(quant), quant)
+    rng = np.random.default_rng(100 + M + 7 * quant)
+    for chunk in range(2):
+        emb = rng.standard_normal((M, 1024)).astype(np.float32)
+        tok, lg = g.prefill_logits(emb)
+        assert o.prefill_batch(emb) == 0
+        x16 = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(o.last_normed())).astype(np.float64)
+        q, sc = o.lm_head_q()
+        ref = (q.astype(np.float64) @ x16) * sc
+        err = float(np.max(np.abs(lg - ref)))
+        assert rel_err(lg, ref) < 2e-3 and cosine(lg, ref) > 0.9999
+        tref = int(np.argmax(ref))
+        assert tok == tref or ref[tref] - ref[tok] <= 2 * err
+        n = (chunk + 1) * M
+        for layer in (0, 1):
+            kg, vg = g.kv_read(layer, 0, n)
+            ko, vo = o.kv_read(layer, 0, n)
+            assert rel_err(kg, ko) < 2e-3 and rel_err(vg, vo) < 2e-3
+    assert g.seq_len == o.seq_len == 2 * M
+
+
 def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models, capfd):
     """A one-launch step whose waits give up (forced here with a 1-round spin
     limit, as a grid that is not co-resident would) reports the timeout in the
