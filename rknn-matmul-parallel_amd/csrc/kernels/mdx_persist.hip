@@ -561,9 +561,13 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         // ================= B: QK-norm, RoPE, KV append, partial attention ==========
         uint4 wE[SE::NW];
         {
+            // q (values 0..255, threads < 128) is needed by every split; the
+            // new k and v only by the split holding position pos, so the
+            // others wait for the 16 q writers alone
+            const bool need = t < 128 || has_new;
             int wd[1] = {W_QKV + j * 1024 + 4 * t};
             u32x4 v[1];
-            const bool ok = ll_wait<1>(rs, wd, v, ep, dead, spin_lim);
+            const bool ok = ll_wait<1>(rs, wd, v, ep, dead || !need, spin_lim);
             qkv_s[2 * t] = ll_f32(v[0].x, v[0].y);
             qkv_s[2 * t + 1] = ll_f32(v[0].z, v[0].w);
             if (__syncthreads_or(!ok)) dead = true;
