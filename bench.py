@@ -126,6 +126,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-w4", action="store_true", help="skip the W4A16 KV 4096 decode (config 5)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="counter runs: the calibration copy, then the M=60 INT8 prefill only")
     ap.add_argument("--workload", default="fp16_kv512", choices=["fp16_kv512", "w4a16_kv4096"],
                     help="decode workload: fp16 layers at KV 512 (the default line), or W4A16 at "
                          "KV 4096 (decode only)")
@@ -164,6 +166,19 @@ def main() -> int:
             print("bench.py: copy probe failed", file=sys.stderr)
             return 1
         log("probe copy: 3 x 256 MiB device-to-device")
+
+    if args.prefill_only:
+        if mdx.lib().mdx_copy_probe(1 << 28, 3) != 0:
+            print("bench.py: copy probe failed", file=sys.stderr)
+            return 1
+        path8 = model_dir(mdx, "prefill_int8_seed1004", cfg, 1, 1004)
+        dec8 = mdx.Decoder(path8, cfg, "int8", 128)
+        emb = mdx.synth_fill_normal(60 * 1024, mdx.synth_seed(1004, "prefill/emb")).reshape(60, 1024)
+        dec8.time_prefill(emb, 2)
+        pms = dec8.time_prefill(emb, max(1, args.steps))
+        dec8.close()
+        print(json.dumps({"workload": "M=60 INT8 prefill, 28 layers", "ms": round(pms, 4)}), flush=True)
+        return 0
 
     # ---- decode (config: 28-layer greedy, FP16 layers + INT8 lm_head, KV 512) ----
     path16 = model_dir(mdx, "decode_int4_seed1005" if w4 else "decode_fp16_seed1003", cfg,
