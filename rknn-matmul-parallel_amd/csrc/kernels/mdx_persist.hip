@@ -53,16 +53,26 @@ constexpr unsigned kSpinLimit = 1u << 18;   // polling rounds before a wait give
 // exchange buffer layout, in 32-bit words
 constexpr int W_CTRL = 0;                          // [0] step counter
 constexpr int W_QKV = 16;                          // [NKV][512 values][2]
-constexpr int PART_WORDS = 520;                    // m0 l0 m1 l1 (x2) | o0[128] x2 | o1[128] x2
-constexpr int W_PART = W_QKV + NKV * 1024;         // [NKV][GRP][PART_WORDS]
+// Partial attention records of KV head j, laid out for the merge's reads: the
+// merging workgroup (j, s) owns 8 output dimensions c = s & 15 of head
+// hh = s >> 4 and finds the 32 splits' values for them in one 2 KiB run
+// ([hh][c][split][8 values x 2 words]), and the 32 (m, l) pairs in one 512 B
+// run after it.  Every exchange region is read with whole-wave 1 KiB loads
+// (lane-contiguous 16-byte groups): polls scattered over 64-byte lines cost
+// one memory request per lane and were the slowest exchanges (measured:
+// 518 -> 475 us/token over the scattered layouts).
+constexpr int PART_O = 2 * 16 * GRP * 16;           // [2][16][GRP][16] o values
+constexpr int PART_WORDS_J = PART_O + 2 * GRP * 4;  // + [2][GRP][4] (m, l)
+constexpr int W_PART = W_QKV + NKV * 1024;          // [NKV][PART_WORDS_J]
 // The all-to-all exchanges (attention output, hidden state after o and after
 // down, SwiGLU activations) are written in NREP copies; workgroup b reads copy
-// b % NREP, which spreads the reads of one exchange over more memory channels.
-constexpr int NREP = 4;
-constexpr int W_ATT = W_PART + NKV * GRP * PART_WORDS;   // [NREP][QD] fp16
+// b % NREP, which spreads the reads of one exchange over more memory channels
+// (2 copies measured best among 1, 2, 4 and 8).
+constexpr int NREP = 2;
+constexpr int W_ATT = W_PART + NKV * PART_WORDS_J;  // [NREP][QD] fp16
 constexpr int W_HO = W_ATT + NREP * QD;            // [NREP][D][2] hidden after o
-constexpr int W_ACT = W_HO + NREP * 2 * D;         // [NREP][NB][16] fp16 (12 used: 64-byte slots)
-constexpr int W_HD = W_ACT + NREP * NB * 16;       // [NREP][D][2] hidden after down
+constexpr int W_ACT = W_HO + NREP * 2 * D;         // [NREP][NB][12] fp16, writer b at 12 b
+constexpr int W_HD = W_ACT + NREP * NB * 12;       // [NREP][D][2] hidden after down
 constexpr int W_AMAX = W_HD + NREP * 2 * D;        // [NB][4] argmax keys
 constexpr int W_TOTAL = W_AMAX + NB * 4;
 static_assert(W_PART % 4 == 0 && W_ATT % 4 == 0 && W_HO % 4 == 0 && W_ACT % 4 == 0 &&
@@ -114,11 +124,6 @@ __device__ __forceinline__ float ll_f32(unsigned lo, unsigned hi) {
 __device__ __forceinline__ void ll_put(unsigned* xb, int word, unsigned payload, unsigned ep) {
     __hip_atomic_store(xb + word, (payload & 0xffffu) | (ep << 16), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void ll_put_f32(unsigned* xb, int word, float v, unsigned ep) {
-    const unsigned u = __float_as_uint(v);
-    ll_put(xb, word, u & 0xffffu, ep);
-    ll_put(xb, word + 1, u >> 16, ep);
 }
 
 // Four LL words in one 16-byte store (each word still carries its own epoch,
@@ -550,11 +555,18 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         __syncthreads();
         rm_dot<KIND, 16, D>(wA, xs4, red, t);
         __syncthreads();
-        if (t < 16) {
-            float y = red[t * SA::NSPLIT];
-            if (SA::NSPLIT == 2) y = y + red[t * SA::NSPLIT + 1];
-            y = y * sclA;
-            ll_put_f32(xb, W_QKV + j * 1024 + 2 * (s * 16 + t), y, ep);
+        if (wave == 0) {
+            // lanes 0..15 hold rows s*16 + lane; even lanes store two rows in one
+            // 16-byte group (eight stores instead of 32 four-byte ones)
+            float y = 0.0f;
+            if (t < 16) {
+                y = red[t * SA::NSPLIT];
+                if (SA::NSPLIT == 2) y = y + red[t * SA::NSPLIT + 1];
+                y = y * sclA;
+            }
+            const float y1 = __shfl_down(y, 1, 64);
+            if (t < 16 && (t & 1) == 0)
+                ll_put4(rs, W_QKV + j * 1024 + 2 * (s * 16 + t), ll_pack2(y, y1, ep));
         }
         MDX_TRACE(16 * l + 2);
 
@@ -738,37 +750,50 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         {
             // 16-byte stores: thread t < 128 writes values 2t and 2t+1
             const int hh = t >> 7, d = t & 127;
-            const int base = W_PART + (j * GRP + s) * PART_WORDS;
+            const int jb = W_PART + j * PART_WORDS_J;
             float* po = &att_o[0][0][0];
             po[t] = runO;
             __syncthreads();
-            if (t < 128) ll_put4(rs, base + 8 + 4 * t, ll_pack2(po[2 * t], po[2 * t + 1], ep));
-            if (d == 0) ll_put4(rs, base + 4 * hh, ll_pack2(runM, runL, ep));
+            if (t < 128) {
+                // values v, v + 1 of head v >> 7: dimension block dd >> 3, slot dd & 7
+                const int v = 2 * t, h2 = v >> 7, dd = v & 127;
+                ll_put4(rs, jb + ((h2 * 16 + (dd >> 3)) * GRP + s) * 16 + 2 * (dd & 7),
+                        ll_pack2(po[v], po[v + 1], ep));
+            }
+            if (d == 0) ll_put4(rs, jb + PART_O + (hh * GRP + s) * 4, ll_pack2(runM, runL, ep));
         }
         MDX_TRACE(16 * l + 4);
 
         uint4 wF[SF::NW];
 
         // ================= C: merge the 32 partials of KV head j (wave 0) ==========
-        // lane i < 32 holds split i; lanes 32..63 poll the same words and add nothing
+        // lane i < 32 holds split i's (m, l) (lanes 32..63 the same again); the
+        // two 1 KiB loads give lane L the values 2 (L & 3), +1 of splits L >> 2
+        // and 16 + (L >> 2)
         if (wave == 0) {
-            const int hh = s >> 4, d0 = (s & 15) * 8;
-            const int i = lane & 31;
-            const int base = W_PART + (j * GRP + i) * PART_WORDS;
-            int wd[5] = {base + 4 * hh, base + 8 + 256 * hh + 2 * d0, base + 12 + 256 * hh + 2 * d0,
-                         base + 16 + 256 * hh + 2 * d0, base + 20 + 256 * hh + 2 * d0};
-            u32x4 v[5];
-            if (!ll_wait<5>(rs, wd, v, ep, dead, spin_lim)) dead = true;
-            const bool mine = lane < 32;
-            const float m = mine ? ll_f32(v[0].x, v[0].y) : -INFINITY;
+            const int hh = s >> 4, c = s & 15, d0 = c * 8;
+            const int jb = W_PART + j * PART_WORDS_J;
+            const int ob = jb + (hh * 16 + c) * GRP * 16;
+            int wd[3] = {jb + PART_O + (hh * GRP + (lane & 31)) * 4, ob + 4 * lane, ob + 256 + 4 * lane};
+            u32x4 v[3];
+            if (!ll_wait<3>(rs, wd, v, ep, dead, spin_lim)) dead = true;
+            const float m = ll_f32(v[0].x, v[0].y);
             const float M = half_max_dpp(m);
             const float w = m == -INFINITY ? 0.0f : exp2_fast(m - M);
-            const float Ls = half_sum_dpp(mine ? ll_f32(v[0].z, v[0].w) * w : 0.0f);
+            const float Ls = half_sum_dpp(ll_f32(v[0].z, v[0].w) * w);
+            const float wa = __shfl(w, lane >> 2, 64), wb = __shfl(w, 16 + (lane >> 2), 64);
+            float p0 = ll_f32(v[1].x, v[1].y) * wa + ll_f32(v[2].x, v[2].y) * wb;
+            float p1 = ll_f32(v[1].z, v[1].w) * wa + ll_f32(v[2].z, v[2].w) * wb;
+#pragma unroll
+            for (int off = 4; off < 64; off <<= 1) {   // sum over the 16 lanes of each slot pair
+                p0 = p0 + __shfl_xor(p0, off, 64);
+                p1 = p1 + __shfl_xor(p1, off, 64);
+            }
             float O[8];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                O[2 * k] = half_sum_dpp(mine ? ll_f32(v[1 + k].x, v[1 + k].y) * w : 0.0f);
-                O[2 * k + 1] = half_sum_dpp(mine ? ll_f32(v[1 + k].z, v[1 + k].w) * w : 0.0f);
+                O[2 * k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p0), k));
+                O[2 * k + 1] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p1), k));
             }
             if (lane < 2 * NREP) {   // lane: copy lane / 2, half lane % 2
                 const unsigned e = ep << 16;
@@ -793,12 +818,13 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         // ================= D: o projection + residual ==========
         const float sclD = Ly.so ? Ly.so[4 * b + (t & 3)] : 1.0f;
         {
-            // waves 1 and 2 gather the attention output
+            // waves 1 and 2 gather the attention output: thread u reads the
+            // 16-byte groups u + 128 k (4 values each), k < 4
             bool ok = true;
             if (wave == 1 || wave == 2) {
                 const int u = t - 64;
-                const int wb = W_ATT + (b % NREP) * QD + 16 * u;
-                int wd[4] = {wb, wb + 4, wb + 8, wb + 12};
+                const int wb = W_ATT + (b % NREP) * QD + 4 * u;
+                int wd[4] = {wb, wb + 512, wb + 1024, wb + 1536};
                 u32x4 v[4];
                 ok = ll_wait_probe<4>(rs, wd, v, ep, dead, spin_lim);
                 uint4 x0, x1;
@@ -810,8 +836,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 x1.y = (v[2].z & 0xffffu) | (v[2].w << 16);
                 x1.z = (v[3].x & 0xffffu) | (v[3].y << 16);
                 x1.w = (v[3].z & 0xffffu) | (v[3].w << 16);
-                xs4[2 * u] = x0;
-                xs4[2 * u + 1] = x1;
+                uint2* x2 = reinterpret_cast<uint2*>(xs4);
+                x2[u] = make_uint2(x0.x, x0.y);
+                x2[u + 128] = make_uint2(x0.z, x0.w);
+                x2[u + 256] = make_uint2(x1.x, x1.y);
+                x2[u + 384] = make_uint2(x1.z, x1.w);
             }
             if (__syncthreads_or(!ok || dead)) dead = true;   // wave 0 may have timed out in C
         }
@@ -872,7 +901,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 pk.y = (c == 0 ? av[1] : c == 1 ? av[5] : av[9]) | e;
                 pk.z = (c == 0 ? av[2] : c == 1 ? av[6] : av[10]) | e;
                 pk.w = (c == 0 ? av[3] : c == 1 ? av[7] : av[11]) | e;
-                ll_put4(rs, W_ACT + (lane / 3) * (NB * 16) + 16 * b + 4 * c, pk);
+                ll_put4(rs, W_ACT + (lane / 3) * (NB * 12) + 12 * b + 4 * c, pk);
             }
         }
         MDX_TRACE(16 * l + 9);
@@ -881,8 +910,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         const float sclF = Ly.sdown ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
         MDX_TRACE(16 * l + 15);
         {
-            const int wb = W_ACT + (b % NREP) * (NB * 16) + 16 * t;
-            int wd[3] = {wb, wb + 4, wb + 8};
+            // thread t reads the 16-byte groups t, t + 256, t + 512; group g
+            // holds the activations 4 g .. 4 g + 3
+            const int wb = W_ACT + (b % NREP) * (NB * 12) + 4 * t;
+            int wd[3] = {wb, wb + 1024, wb + 2048};
             u32x4 v[3];
             const bool ok = ll_wait_probe<3>(rs, wd, v, ep, dead, spin_lim);
             uint2* x2 = reinterpret_cast<uint2*>(xs4);
@@ -891,7 +922,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 uint2 p;
                 p.x = (v[k].x & 0xffffu) | (v[k].y << 16);
                 p.y = (v[k].z & 0xffffu) | (v[k].w << 16);
-                x2[3 * t + k] = p;
+                x2[t + 256 * k] = p;
             }
             if (__syncthreads_or(!ok)) dead = true;
         }
