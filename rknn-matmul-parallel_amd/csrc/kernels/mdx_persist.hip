@@ -826,7 +826,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 const int wb = W_ATT + (b % NREP) * QD + 4 * u;
                 int wd[4] = {wb, wb + 512, wb + 1024, wb + 1536};
                 u32x4 v[4];
-                ok = ll_wait_probe<4>(rs, wd, v, ep, dead, spin_lim);
+                ok = ll_wait<4>(rs, wd, v, ep, dead, spin_lim);
                 uint4 x0, x1;
                 x0.x = (v[0].x & 0xffffu) | (v[0].y << 16);
                 x0.y = (v[0].z & 0xffffu) | (v[0].w << 16);

@@ -320,7 +320,12 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_s(const uint16_t* __restrict__
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int tile = blockIdx.x, split = blockIdx.y;
+    // Blocks id, id + 8, id + 16, ... run on one XCD (one L2).  Each XCD takes a
+    // contiguous run of (split, tile) pairs, so it fetches one or two splits'
+    // activation panels instead of all of them.
+    const int ntile = N / (16 * NW), nb = gridDim.x, id = blockIdx.x;
+    const int gi = (nb & 7) ? id : (id & 7) * (nb >> 3) + (id >> 3);
+    const int tile = gi % ntile, split = gi / ntile;
     const int k0 = split * kKS;
     const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
     const int wrow = (tile * NW + wave) * 16 + c16;      // this lane's weight row
@@ -700,7 +705,7 @@ static bool gemm_s_ok(int M, const mdx_wdesc* w) {
 }
 
 static int gemm_s_launch(const uint16_t* x16, int M, const mdx_wdesc* w, float* part, void* stream) {
-    dim3 grid(w->N / 64, w->K / kKS);
+    dim3 grid((w->N / 64) * (w->K / kKS));   // (split, tile) pairs, decoded in the kernel
     const uint8_t* wp = (const uint8_t*)w->w;
     hipStream_t s = (hipStream_t)stream;
     switch (w->kind) {
