@@ -717,6 +717,11 @@ static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
     c->pargs.cooperative = c->persist_coop;
     c->pargs.spin_limit = c->spin_once;
     c->spin_once = 0;
+    /* K/V rows of a long context are streamed past the last-level cache
+     * (256 MB), which then keeps the 156 MB INT8 lm_head from step to step;
+     * a short context's rows (read again every step) stay cached */
+    const double kv_bytes = 2.0 * c->L * (double)(c->seq_len + 1) * c->kvd * 2.0;
+    c->pargs.kv_stream = kv_bytes > 96.0 * 1024 * 1024;
     return mdx_launch_persist_step(&c->pargs, c->stream);
 }
 

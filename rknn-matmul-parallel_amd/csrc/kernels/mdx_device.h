@@ -172,6 +172,9 @@ typedef struct {
     unsigned long long* trace;         /* optional [256][trace_stride] timestamps */
     int trace_stride;                  /* >= mdx_persist_trace_events(n_layers) */
     unsigned spin_limit;               /* polling rounds before a wait gives up; 0: default */
+    int kv_stream;                     /* 1: read the K/V rows with non-temporal loads (a
+                                          cache too large to stay in the last-level cache
+                                          next to the lm_head) */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */
