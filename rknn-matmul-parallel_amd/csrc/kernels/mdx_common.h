@@ -25,6 +25,14 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
+// Non-temporal 16-byte load, for data read once per step or per launch
+// (weights streamed past the caches): it does not evict what is read again.
+__device__ __forceinline__ uint4 ld_nt(const void* p) {
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 

@@ -181,7 +181,7 @@ struct RowSet {
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int j = base + u * 64 + lane;
-                wv[r][u] = (valid[r] && j < nchunks) ? rp[j] : make_uint4(0, 0, 0, 0);
+                wv[r][u] = (valid[r] && j < nchunks) ? ld_nt(rp + j) : make_uint4(0, 0, 0, 0);
             }
         }
     }

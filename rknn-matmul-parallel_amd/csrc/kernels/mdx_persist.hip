@@ -233,15 +233,11 @@ __device__ __forceinline__ unsigned step_epoch(unsigned E, int L, int l) {
 
 // ---- weights ----------------------------------------------------------------
 
-// Non-temporal 16-byte load.  The layer weights (and, for long contexts, the
-// K/V rows) are read once per step and would otherwise evict what is read
-// again every step from the last-level cache: the lm_head and a short
+// The layer weights (and, for long contexts, the K/V rows) are read once per
+// step with non-temporal loads (ld_nt), so they do not evict from the
+// last-level cache what is read again every step: the lm_head and a short
 // context's K/V rows (measured: 480 -> 470 us/token at KV 512 with the layer
 // weights non-temporal; at KV 4096 the K/V rows non-temporal too, 569 -> 550).
-__device__ __forceinline__ uint4 ld_nt(const void* p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 template <int KIND> struct KT;
 template <> struct KT<MDX_W_F16> { static constexpr int E = 8; };

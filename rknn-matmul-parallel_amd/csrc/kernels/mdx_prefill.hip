@@ -18,6 +18,11 @@ namespace {
 
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
+// Weights are read once per prefill: non-temporal loads keep them from
+// evicting the activation panels and split-K partials that the following
+// kernels read again (measured: 1.139 -> 1.089 ms for the M=60 INT8 prefill).
+__device__ __forceinline__ uint4 ld_w(const void* p) { return ld_nt(p); }
+
 constexpr int kMaxM = 64;
 constexpr int kNT = 32;        // weight rows (output columns) per block
 
@@ -137,7 +142,7 @@ __device__ __forceinline__ void gemm_issue(GemmRound<KIND>& R, int kb, int kb_la
         const int k = min(kb + j, kb_last) * KB + g * EPL;
 #pragma unroll
         for (int t = 0; t < 2; t++)
-            R.bw[j][t] = wvalid[t] ? *reinterpret_cast<const uint4*>(wrow[t] + (size_t)k * 16 / EPL)
+            R.bw[j][t] = wvalid[t] ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
                                    : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int r = 0; r < 4; r++)
@@ -333,7 +338,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_s(const uint16_t* __restrict__
     {
         const uint8_t* wr = w + (size_t)wrow * row_bytes + (size_t)(k0 + g * EPL) * 16 / EPL;
 #pragma unroll
-        for (int j = 0; j < NCH; j++) wv[j] = *reinterpret_cast<const uint4*>(wr + (size_t)j * CK * 16 / EPL);
+        for (int j = 0; j < NCH; j++) wv[j] = ld_w(wr + (size_t)j * CK * 16 / EPL);
     }
     // the panel: 64 rows (rows >= M repeat row M-1) x kKS fp16
     {
