@@ -19,9 +19,11 @@ shapes); and the oracle (the scalar C restatement of the reference CPU path)
 timed on this host on a bounded sample of the same decode workload.  The
 other workloads of the metric each get their own object under "configs":
   1  one INT8 GEMV tile 1 x 1024 x 4096 with per-column scales, 1024
-     back-to-back launches over 128 rotated weight copies (541 MB);
+     back-to-back launches over 128 rotated weight copies (541 MB), replayed
+     from a captured graph of 128 launches;
   2  one fp16 layer's seven projections with their RMSNorms at M = 1 (four
-     launches), cycling through the 28 layers of the decode model;
+     launches), cycling through the 28 layers of the decode model (a captured
+     graph of the 28 layers' 112 launches, replayed);
   4  the M=60 INT8 batch prefill (28 layers, 60 tokens from an empty cache);
   5  W4A16 greedy decode at KV 4096 -> 4224 (128 steps), int4 layer weights
      with fp16 scales, INT8 lm_head.
@@ -243,7 +245,7 @@ def main() -> int:
             "avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
             "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
             "kernels": "k_gemv: RMSNorm+q|k|v, o+residual, RMSNorm+gate|up+SwiGLU, down+residual",
-            "rotation": "28 layers' distinct weights (881 MB)"}
+            "rotation": "28 layers' distinct weights (881 MB), launches replayed from a captured graph"}
         log(f"config 2 layer projections: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
         # ---- config 1: the INT8 lm_head tile GEMV 1 x 1024 x 4096 ----
         us1 = mdx.time_gemv(1, 1024, 4096, 128, 1024)
@@ -252,7 +254,7 @@ def main() -> int:
             "avg_us": round(us1, 3), "bytes": b1, "GBps": round(b1 / us1 / 1e3, 1),
             "hbm_frac": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 4),
             "kernels": "k_gemv<int8> (fp32 x rounded to fp16, per-column scales)",
-            "rotation": "1024 launches over 128 weight copies (541 MB)"}
+            "rotation": "1024 launches over 128 weight copies (541 MB), replayed from a captured graph"}
         log(f"config 1 int8 tile GEMV: {us1:.2f} us, {b1 / us1 / 1e3:.0f} GB/s")
 
     # ---- batch prefill M=60 through 28 INT8 layers ----

@@ -101,8 +101,10 @@ int mdx_time_prefill(MatmulDecoderContext* ctx, const float* embeddings, int M, 
 /* Average device microseconds of one GEMV y = fp16(x) . W (x per-column
  * scale) with kind 1 (int8) or 0 (fp16) weights of [K,N], timed with HIP
  * events over `iters` back-to-back launches that cycle through `copies`
- * distinct weight buffers (enough copies defeat the device caches).  The
- * buffers hold a fixed pattern; the kernel is the decoder's per-stage GEMV. */
+ * distinct weight buffers (enough copies defeat the device caches), issued
+ * from a captured graph of one launch per copy when iters is a multiple of
+ * copies (MDX_GRAPHS=0: one by one).  The buffers hold a fixed pattern; the
+ * kernel is the decoder's per-stage GEMV. */
 int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us);
 
 /* ---- single-kernel entry points (weights in the on-disk layout) ---- */

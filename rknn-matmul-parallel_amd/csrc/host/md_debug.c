@@ -119,16 +119,38 @@ int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us) 
         rc = mdxrt_fill_u32(buf + per * i + wb, 0x3b800000u, (size_t)N, s);
     if (!rc) rc = mdxrt_fill_u32(dx, 0x3f800000u, (size_t)K, s);
     mdx_wdesc w = {NULL, NULL, dk, K, N};
-    for (int i = 0; i < 8 && !rc; i++) {   /* warm-up */
+    /* The launches go back to back from a captured graph of one launch per
+     * weight copy (replayed iters / copies times), so the host's launch
+     * overhead is not what is timed; MDX_GRAPHS=0 issues them one by one. */
+    const char* ge = getenv("MDX_GRAPHS");
+    const int use_graph = !(ge && ge[0] == '0') && iters % copies == 0;
+    void* g = NULL;
+    if (!rc && use_graph) {
+        rc = mdxrt_graph_begin(s);
+        int rc2 = 0;
+        for (int i = 0; i < copies && !rc2; i++) {
+            w.w = buf + per * i;
+            w.scale = (const float*)(buf + per * i + wb);
+            rc2 = mdx_launch_gemv(dx, &w, 0, dy, s);
+        }
+        if (!rc) rc = mdxrt_graph_end(s, &g);
+        if (rc2) rc = rc2;
+        if (!rc) rc = mdxrt_graph_launch(g, s);   /* warm-up */
+    }
+    for (int i = 0; i < 8 && !rc && !use_graph; i++) {   /* warm-up */
         w.w = buf + per * (i % copies);
         w.scale = (const float*)(buf + per * (i % copies) + wb);
         rc = mdx_launch_gemv(dx, &w, 0, dy, s);
     }
     if (!rc) rc = mdxrt_event_record(e0, s);
-    for (int i = 0; i < iters && !rc; i++) {
-        w.w = buf + per * (i % copies);
-        w.scale = (const float*)(buf + per * (i % copies) + wb);
-        rc = mdx_launch_gemv(dx, &w, 0, dy, s);
+    if (use_graph) {
+        for (int i = 0; i < iters / copies && !rc; i++) rc = mdxrt_graph_launch(g, s);
+    } else {
+        for (int i = 0; i < iters && !rc; i++) {
+            w.w = buf + per * (i % copies);
+            w.scale = (const float*)(buf + per * (i % copies) + wb);
+            rc = mdx_launch_gemv(dx, &w, 0, dy, s);
+        }
     }
     if (!rc) rc = mdxrt_event_record(e1, s);
     if (!rc) rc = mdxrt_stream_sync(s);
@@ -136,6 +158,7 @@ int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us) 
     if (!rc) rc = mdxrt_event_elapsed_ms(e0, e1, &ms);
     if (!rc) *avg_us = ms * 1000.0f / iters;
     if (s) mdxrt_stream_sync(s);
+    if (g) mdxrt_graph_destroy(g);
     mdxrt_free(buf);
     mdxrt_free(dx);
     mdxrt_free(dy);

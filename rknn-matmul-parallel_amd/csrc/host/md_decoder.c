@@ -1482,6 +1482,10 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
     return 0;
 }
 
+static int time_projection_launch(MatmulDecoderContext* c, int sel, int l, const mdx_wdesc* w0,
+                                  float eps);
+static int time_projection_bytes(const MatmulDecoderContext* c, int sel, double* bytes);
+
 int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, float* avg_us,
                         double* bytes) {
     if (!c || !which || iters <= 0) return MATMUL_DECODER_ERR_INVALID_ARG;
@@ -1495,33 +1499,58 @@ int mdx_time_projection(MatmulDecoderContext* c, const char* which, int iters, f
     if (sel < 0 || (sel == 4 && c->n_lm > 1)) return MATMUL_DECODER_ERR_INVALID_ARG;
     const float eps = c->config.rms_eps;
     const mdx_wdesc* w0 = sel == 4 ? &c->lm : NULL;
-    int rc = mdxrt_event_record(c->ev0, c->stream);
-    for (int i = 0; i < iters && !rc; i++) {
-        md_layer* ly = &c->layers[i % c->L];
-        switch (sel) {
-            case 0: rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_tmp, c->stream); break;
-            case 1: rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream); break;
-            case 2: rc = mdx_launch_norm_gemv(c->d_hidden, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream); break;
-            case 3: rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream); break;
-            case 5:
-                /* the seven projections of one layer with their RMSNorms: merged
-                 * q|k|v, o (+residual), merged gate|up (+SwiGLU), down (+residual) */
-                rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_qkv, c->stream);
-                if (!rc) rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream);
-                if (!rc) rc = mdx_launch_norm_gemv(c->d_tmp, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream);
-                if (!rc) rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream);
-                break;
-            default:
-                rc = mdx_launch_lmhead(c->d_hidden, c->d_final_norm, eps, w0, c->d_logits,
-                                       c->d_partial, c->d_state, NULL, 0, c->stream);
-        }
+    /* the per-layer selections replay a captured graph of one pass over the
+     * layers when iters is a multiple of the layer count, so the host's launch
+     * overhead is not what is timed */
+    const int use_graph = c->use_graphs && sel != 4 && iters % c->L == 0;
+    void* g = NULL;
+    int rc = 0;
+    if (use_graph) {
+        rc = mdxrt_graph_begin(c->stream);
+        int rc2 = 0;
+        for (int l = 0; l < c->L && !rc2; l++) rc2 = time_projection_launch(c, sel, l, w0, eps);
+        if (!rc) rc = mdxrt_graph_end(c->stream, &g);
+        if (rc2) rc = rc2;
+        if (!rc) rc = mdxrt_graph_launch(g, c->stream);   /* warm-up */
     }
+    if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
+    for (int i = 0; i < iters / c->L && !rc && use_graph; i++) rc = mdxrt_graph_launch(g, c->stream);
+    for (int i = 0; i < iters && !rc && !use_graph; i++) rc = time_projection_launch(c, sel, i % c->L, w0, eps);
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
+    if (g) mdxrt_graph_destroy(g);
     if (rc) return MATMUL_DECODER_ERR_RKNN;
     float ms = 0.0f;
     mdxrt_event_elapsed_ms(c->ev0, c->ev1, &ms);
     if (avg_us) *avg_us = ms * 1000.0f / iters;
+    return time_projection_bytes(c, sel, bytes);
+}
+
+static int time_projection_launch(MatmulDecoderContext* c, int sel, int l, const mdx_wdesc* w0,
+                                  float eps) {
+    int rc = 0;
+    md_layer* ly = &c->layers[l];
+    switch (sel) {
+        case 0: rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_tmp, c->stream); break;
+        case 1: rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream); break;
+        case 2: rc = mdx_launch_norm_gemv(c->d_hidden, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream); break;
+        case 3: rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream); break;
+        case 5:
+            /* the seven projections of one layer with their RMSNorms: merged
+             * q|k|v, o (+residual), merged gate|up (+SwiGLU), down (+residual) */
+            rc = mdx_launch_norm_gemv(c->d_hidden, ly->in_norm, eps, &ly->qkv, 0, c->d_qkv, c->stream);
+            if (!rc) rc = mdx_launch_gemv_add(c->d_attn16, &ly->o, c->d_tmp, c->stream);
+            if (!rc) rc = mdx_launch_norm_gemv(c->d_tmp, ly->post_norm, eps, &ly->gu, 1, c->d_act16, c->stream);
+            if (!rc) rc = mdx_launch_gemv_add(c->d_act16, &ly->down, c->d_tmp, c->stream);
+            break;
+        default:
+            rc = mdx_launch_lmhead(c->d_hidden, c->d_final_norm, eps, w0, c->d_logits,
+                                   c->d_partial, c->d_state, NULL, 0, c->stream);
+    }
+    return rc;
+}
+
+static int time_projection_bytes(const MatmulDecoderContext* c, int sel, double* bytes) {
     if (bytes && sel == 5) {
         /* weights and scales of the four launches, the two norm vectors, and
          * the activations each one reads and writes */
