@@ -50,6 +50,11 @@ int mdx_decode_path(const MatmulDecoderContext* ctx);
  * times before giving up (0: the default), which forces the timeout-and-retry
  * path without any workgroup waiting long. */
 int mdx_debug_persist_spin_limit(MatmulDecoderContext* ctx, unsigned rounds);
+/* Test hook: how the one-launch step reads the K/V rows.  -1 (the default):
+ * with non-temporal loads once the cache holds more than 96 MB, so that a long
+ * context does not evict the lm_head from the last-level cache; 0 / 1: always
+ * ordinary / always non-temporal.  The results are the same either way. */
+int mdx_debug_persist_kv_stream(MatmulDecoderContext* ctx, int mode);
 /* Test hook: before the next cooperative retry, leave exchange words tagged
  * with the epoch that retry would accept first (what a workgroup of the
  * timed-out launch that started late could have written); the retry must

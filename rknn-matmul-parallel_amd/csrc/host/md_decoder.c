@@ -70,6 +70,7 @@ struct MatmulDecoderContext {
     int persist_coop;        /* 1: launch it cooperatively (after an ordinary launch timed out) */
     unsigned spin_once;      /* test hook: spin limit of the next one-launch step (0: default) */
     int poison_retry;        /* test hook: plant stale exchange words before the next retry */
+    int kv_stream_force;     /* test hook: -1 decide per launch; 0 / 1 force the K/V load policy */
     int profile;             /* MDX_PROFILE=1: per-stage stats from device timestamps */
     unsigned long long* d_trace;   /* [256][trace_ev] timestamps of the profiled step */
     unsigned long long* h_trace;
@@ -721,7 +722,7 @@ static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
      * (256 MB), which then keeps the 156 MB INT8 lm_head from step to step;
      * a short context's rows (read again every step) stay cached */
     const double kv_bytes = 2.0 * c->L * (double)(c->seq_len + 1) * c->kvd * 2.0;
-    c->pargs.kv_stream = kv_bytes > 96.0 * 1024 * 1024;
+    c->pargs.kv_stream = c->kv_stream_force >= 0 ? c->kv_stream_force : kv_bytes > 96.0 * 1024 * 1024;
     return mdx_launch_persist_step(&c->pargs, c->stream);
 }
 
@@ -895,6 +896,7 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     {
         const char* e = getenv("MDX_PROFILE");
         c->profile = e && e[0] == '1';
+        c->kv_stream_force = -1;
     }
     if (c->profile && c->persist) {
         c->trace_ev = mdx_persist_trace_events(c->L);
@@ -1656,6 +1658,13 @@ int mdx_debug_persist_spin_limit(MatmulDecoderContext* c, unsigned rounds) {
     if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
     if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
     c->spin_once = rounds;
+    return 0;
+}
+
+int mdx_debug_persist_kv_stream(MatmulDecoderContext* c, int mode) {
+    if (!c || mode < -1 || mode > 1) return MATMUL_DECODER_ERR_INVALID_ARG;
+    if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
+    c->kv_stream_force = mode;
     return 0;
 }
 

@@ -85,6 +85,32 @@ def test_step_matches_oracle(mdx, gpu, oracle_lib, models, quant, n_pos):
     assert g.seq_len == n_pos + 1
 
 
+@pytest.mark.parametrize("n_pos", [33, 600, 4100])
+def test_kv_load_policy_is_bit_identical(mdx, gpu, oracle_lib, models, n_pos):
+    """The K/V rows read with ordinary or with non-temporal loads (the policy
+    the host picks by cache size) give the same bits: logits, token and the
+    appended K/V row, over three steps."""
+    cfg, get = models
+    path = get(0)
+    runs = []
+    for mode in (0, 1):
+        g, _ = _pair(mdx, oracle_lib, cfg, path, 0)
+        g.force_kv_stream(mode)
+        g.kv_fill_normal(n_pos, 91)
+        out = []
+        tok = 1234
+        for _ in range(3):
+            tok, lg = g.step(tok)
+            out.append((tok, lg.copy()))
+        k, v = g.kv_read(1, n_pos, 3)
+        runs.append((out, k.copy(), v.copy()))
+        g.close()
+    (a, ka, va), (b, kb, vb) = runs
+    for (ta, la), (tb, lb) in zip(a, b):
+        assert ta == tb and np.array_equal(la, lb)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
 @pytest.mark.parametrize("quant", [0, 1, 2])
 def test_one_launch_matches_per_stage_path(mdx, gpu, oracle_lib, models, quant):
     cfg, get = models
