@@ -121,6 +121,13 @@ int mdx_time_gemv(int kind, int K, int N, int copies, int iters, float* avg_us);
 int mdx_debug_gemv(int kind, int K, int N, const void* w, const float* scales, const float* x,
                    float* y);
 /* M-row MFMA projection, M <= 64: y[M,N] = fp16(x[M,K]) . W (x scale). */
+/* One residual projection of the batch prefill (the o and down stages):
+ * hidden[M][N] += fp16(x) . W (x scale), then x16_out[M][N] =
+ * fp16((hidden * rms) * norm_w) per row when norm_w is given.  kind and the
+ * weight / scale formats as mdx_debug_gemm; hidden is updated in place. */
+int mdx_debug_gemm_residual(int kind, int M, int K, int N, const void* w, const float* scales,
+                            const float* x, float* hidden, const float* norm_w, float eps,
+                            uint16_t* x16_out);
 int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* scales,
                    const float* x, float* y);
 /* One decode attention layer at position pos: qkv fp32 [nq*hd + 2*nkv*hd]

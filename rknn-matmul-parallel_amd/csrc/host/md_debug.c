@@ -191,6 +191,35 @@ int mdx_debug_gemm(int kind, int M, int K, int N, const void* w, const float* sc
     return scope_close(&s, rc);
 }
 
+int mdx_debug_gemm_residual(int kind, int M, int K, int N, const void* w, const float* scales,
+                            const float* x, float* hidden, const float* norm_w, float eps,
+                            uint16_t* x16_out) {
+    if (kind < 0 || kind > 2 || M <= 0 || M > 64 || K <= 0 || N <= 0 || !w || !x || !hidden ||
+        (norm_w && !x16_out))
+        return MATMUL_DECODER_ERR_INVALID_ARG;
+    dbg_scope s;
+    int rc = scope_open(&s);
+    if (rc) return rc;
+    mdx_wdesc d;
+    rc = upload_weights(&s, kind, K, N, w, scales, &d);
+    float* dx = rc ? NULL : (float*)dalloc(&s, (size_t)M * K * 4);
+    uint16_t* dx16 = rc ? NULL : (uint16_t*)dalloc(&s, (size_t)M * K * 2);
+    float* dh = rc ? NULL : (float*)dalloc(&s, (size_t)M * N * 4);
+    float* dnw = (rc || !norm_w) ? NULL : (float*)dalloc(&s, (size_t)N * 4);
+    uint16_t* dout = (rc || !norm_w) ? NULL : (uint16_t*)dalloc(&s, (size_t)M * N * 2);
+    float* scr = rc ? NULL : (float*)dalloc(&s, mdx_gemm_scratch_floats(M, N, K) * 4);
+    if (!rc && (!dx || !dx16 || !dh || !scr || (norm_w && (!dnw || !dout)))) rc = MATMUL_DECODER_ERR_MEMORY;
+    if (!rc) rc = mdxrt_h2d(dx, x, (size_t)M * K * 4);
+    if (!rc) rc = mdxrt_h2d(dh, hidden, (size_t)M * N * 4);
+    if (!rc && norm_w) rc = mdxrt_h2d(dnw, norm_w, (size_t)N * 4);
+    if (!rc) rc = mdx_launch_to_f16(dx, M * K, dx16, s.stream);
+    if (!rc) rc = mdx_launch_gemm_residual_norm(dx16, M, &d, dh, dnw, eps, dout, scr, s.stream);
+    if (!rc) rc = mdxrt_stream_sync(s.stream);
+    if (!rc) rc = mdxrt_d2h(hidden, dh, (size_t)M * N * 4);
+    if (!rc && norm_w) rc = mdxrt_d2h(x16_out, dout, (size_t)M * N * 2);
+    return scope_close(&s, rc);
+}
+
 static int upload_state(dbg_scope* s, int pos, mdx_state** d_state) {
     mdx_state h;
     memset(&h, 0, sizeof h);

@@ -145,6 +145,8 @@ def lib() -> C.CDLL:
             "mdx_device_synchronize": (C.c_int, []),
             "mdx_debug_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
+            "mdx_debug_gemm_residual": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F,
+                                                  _F, C.c_float, C.POINTER(C.c_uint16)]),
             "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                                 C.c_float, _F, _F, _F, _U16, _U16, _F, _U16, _U16]),
             "mdx_debug_attn_prefill": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _F, _U16,
@@ -262,6 +264,21 @@ def gemm(kind: int, M: int, K: int, N: int, w: np.ndarray, scales, x) -> np.ndar
     _check(lib().mdx_debug_gemm(kind, M, K, N, w.ctypes.data, _p(s, _F), _p(x, _F), _p(y, _F)),
            "gemm")
     return y.reshape(M, N)
+
+
+def gemm_residual(kind: int, M: int, K: int, N: int, w: np.ndarray, scales, x, hidden, norm_w,
+                  eps: float = 1e-6):
+    """Prefill residual projection: (hidden + fp16(x) . W * scale, fp16 normed rows or None)."""
+    w = np.ascontiguousarray(w)
+    s, x = _f32(scales), _f32(x)
+    h = np.array(_f32(hidden), dtype=np.float32, copy=True).reshape(M, N)
+    nw = _f32(norm_w)
+    out = np.zeros((M, N), np.uint16) if norm_w is not None else None
+    _check(lib().mdx_debug_gemm_residual(kind, M, K, N, w.ctypes.data, _p(s, _F), _p(x, _F),
+                                         _p(h, _F), _p(nw, _F), eps,
+                                         out.ctypes.data_as(C.POINTER(C.c_uint16)) if out is not None
+                                         else None), "gemm_residual")
+    return h, out
 
 
 def attn_decode(nq, nkv, hd, pos, style, theta, eps, q_norm, k_norm, qkv, k16, v16):

@@ -111,6 +111,41 @@ def test_gemm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
     assert rel_err(y, ref) < TOL * 0.1
 
 
+# The o / down stages of the prefill: split-K over 256-K blocks with the block
+# order grouped per XCD (N/64 x K/256 a multiple of 8: (60,2048,1024),
+# (60,3072,1024), (5,4096,192), (33,1024,4096)), the plain order otherwise
+# ((17,768,960): 45 blocks; (64,256,64): one block), and K not a multiple of
+# 256 (the k_gemm path: (9,320,128)).  hidden += x.W*s is checked against the
+# oracle's projection; the fp16 normed rows against numpy on the returned
+# hidden (one fp16 ulp).
+@pytest.mark.parametrize("kind", [0, 1, 2])
+@pytest.mark.parametrize("M,K,N", [(60, 2048, 1024), (60, 3072, 1024), (5, 4096, 192), (33, 1024, 4096),
+                                   (17, 768, 960), (64, 256, 64), (9, 320, 128)])
+def test_gemm_residual_norm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
+    if kind == 2 and K % 128:
+        pytest.skip("int4 projections take K in multiples of 128")
+    rng = np.random.default_rng(M * 7 + K * 3 + N + kind)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if kind == 0:
+        w, s = _f16_bits(rng.standard_normal((K, N)) * 0.02), None
+    elif kind == 1:
+        w, s = rng.integers(-127, 128, (K, N)).astype(np.int8), rng.uniform(1e-4, 2e-4, N).astype(np.float32)
+    else:
+        w, s = _pack_i4(rng.integers(-8, 8, (K, N))), rng.uniform(1e-3, 3e-3, N).astype(np.float32)
+    h0 = rng.standard_normal((M, N)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    h, x16 = mdx.gemm_residual(kind, M, K, N, w, s, x, h0, nw)
+    y = oracle_lib.matmul(kind, x, w, s, M, K, N)
+    assert rel_err(h - h0, y) < TOL * 0.1, f"projection rel err {rel_err(h - h0, y):.2e}"
+    assert np.allclose(h, h0 + y, rtol=1e-5, atol=1e-5 * float(np.abs(y).max()))
+    rms = 1.0 / np.sqrt((h.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    ref16 = ((h * rms) * nw).astype(np.float16).view(np.uint16).astype(np.int32)
+    ulp = np.abs(x16.astype(np.int32) - ref16)
+    assert ulp.max() <= 1, f"normed rows differ by {ulp.max()} fp16 ulp"
+    h2, none = mdx.gemm_residual(kind, M, K, N, w, s, x, h0, None)
+    assert none is None and np.array_equal(h2, h)
+
+
 def test_gemm_int8_known_answer_bit_exact(mdx, gpu):
     rng = np.random.default_rng(77)
     M, K, N = 60, 3072, 256
