@@ -820,12 +820,19 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             }
         }
         // The remaining gate/up and the down weights are requested once the
-        // merge is done, by every wave: a burst issued while the partial
-        // records are in flight delays them (measured: 522 -> 510 us/token
-        // against requesting from waves 1..3 before the merge).
+        // merge is done: a burst issued while the partial records are in
+        // flight delays them (measured: 522 -> 510 us/token against requesting
+        // from waves 1..3 before the merge).  With fp16 weights (the largest
+        // burst) waves 1 and 2, which gather the attention output next,
+        // request theirs after that gather, so their polls do not wait behind
+        // the weights (478.0 -> 475.6 us/token; with int8 or int4 weights the
+        // same split costs 6-8 us, so there every wave requests here).
+        constexpr bool kSplitReq = KIND == MDX_W_F16;
         __syncthreads();
-        rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
-        cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
+        if (!kSplitReq || wave == 0 || wave == 3) {
+            rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+            cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
+        }
         MDX_TRACE(16 * l + 5);
 
         // ================= D: o projection + residual ==========
@@ -854,6 +861,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 x2[u + 128] = make_uint2(x0.z, x0.w);
                 x2[u + 256] = make_uint2(x1.x, x1.y);
                 x2[u + 384] = make_uint2(x1.z, x1.w);
+                if (kSplitReq) {
+                    rm_load<KIND, 24, D>(wE, Ly.wgu, rowE, t, SE::NW / 2, SE::NW);
+                    cm_load<KIND, 4, FF>(wF, Ly.wdown, 4 * b, t);
+                }
             }
             if (__syncthreads_or(!ok || dead)) dead = true;   // wave 0 may have timed out in C
         }
