@@ -119,6 +119,36 @@ def run_cpu_baseline(path: str, d: dict, budget_s: float) -> dict:
             **info}
 
 
+def run_sampling(mdx, cfg, max_seq: int, args) -> int:
+    """Per-step time of device-side sampling (matmul_decoder_step_sample,
+    logits left on the device) against greedy steps (mdx_step_token), each
+    over `--steps` steps after two untimed ones, KV refilled to 512 first."""
+    path16 = model_dir(mdx, "decode_fp16_seed1003", cfg, 0, 1003)
+    dec = mdx.Decoder(path16, cfg, "fp16", max_seq + 64)
+    lib = mdx.lib()
+    n = max(4, args.steps)
+
+    def per_step(fn):
+        dec.kv_fill_normal(KV_PREFILL, 1003)
+        fn()
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return (time.perf_counter() - t0) * 1000.0 / n
+
+    res = {"greedy_ms": round(per_step(lambda: dec.step_token(5)), 4)}
+    hist = list(range(100, 164))
+    for k in (40, 64, 1024):
+        p, toks = mdx.sampling_params(k, 0.9, 0.8, 1.1, hist)
+        res[f"top_k_{k}_ms"] = round(per_step(
+            lambda: lib.matmul_decoder_step_sample(dec.h, 5, None, mdx.C.byref(p), 0.37, None)), 4)
+    dec.close()
+    print(json.dumps({"workload": "sampled decode step, fp16 layers, KV 512, T 0.8, top-p 0.9, "
+                                  "64 penalised tokens", "steps": n, **res}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,6 +163,9 @@ def main() -> int:
     ap.add_argument("--workload", default="fp16_kv512", choices=["fp16_kv512", "w4a16_kv4096"],
                     help="decode workload: fp16 layers at KV 512 (the default line), or W4A16 at "
                          "KV 4096 (decode only)")
+    ap.add_argument("--sampling", action="store_true",
+                    help="sampled decode: matmul_decoder_step_sample at top-k 40, 64 and 1024 (T 0.8, "
+                         "top-p 0.9, 64 penalised tokens) against greedy steps, fp16 layers at KV 512")
     ap.add_argument("--probe", action="store_true",
                     help="counter runs: a 256 MiB device copy (the calibration kernel), then the "
                          "decode steps only")
@@ -181,6 +214,9 @@ def main() -> int:
         dec8.close()
         print(json.dumps({"workload": "M=60 INT8 prefill, 28 layers", "ms": round(pms, 4)}), flush=True)
         return 0
+
+    if args.sampling:
+        return run_sampling(mdx, cfg, max_seq, args)
 
     # ---- decode (config: 28-layer greedy, FP16 layers + INT8 lm_head, KV 512) ----
     path16 = model_dir(mdx, "decode_int4_seed1005" if w4 else "decode_fp16_seed1003", cfg,

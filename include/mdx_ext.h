@@ -201,7 +201,7 @@ int matmul_decoder_step_sample(MatmulDecoderContext* ctx, int token_id, const fl
  * top_k must be in [1, min(V, MDX_SAMPLE_MAX_TOP_K)] (larger k is rejected
  * with a message: the scratch holds 1024 candidates).  Enqueued on `stream`
  * (NULL: the default stream); returns without synchronising.  It calls no
- * allocator: its 13 KB of scratch is a static device array of the library,
+ * allocator: its 141 KB of scratch is a static device array of the library,
  * one per GPU, held until the process ends.  Calls that overlap on one GPU
  * share that scratch and race; serialise them.  Returns 0, -1 for bad
  * arguments, -4 on a HIP failure. */

@@ -1,8 +1,13 @@
 // mdx_sample.hip — token sampling on the device, from the logits a decode step
 // leaves in HBM, so that non-greedy decoding needs no copy of the V logits to
-// the host.  Seven short launches: a scratch clear, four radix-select levels
-// and a gather over 128 workgroups (each owns a contiguous index range), and
-// one finishing workgroup of 1024 threads.
+// the host.  For top_k <= 64 (the usual sampling settings) two launches:
+// 256 workgroups each keep the 64 best of their contiguous index range as
+// 64-bit ranking keys, sorted with wave-level bitonic networks in registers;
+// one workgroup of 1024 threads merges the 256 lists the same way, and the
+// first k keys are the candidates in rank order.  Larger k: seven short
+// launches, a scratch clear, four radix-select levels and a gather over 128
+// workgroups (each owns a contiguous index range), and one finishing
+// workgroup that ranks the candidates with a bitonic sort in LDS.
 //
 //   1. (separate tiny kernel) repetition penalty on the listed tokens, once
 //      per distinct token: a positive logit is divided by the penalty, any
@@ -44,8 +49,12 @@ constexpr int kThreads = 1024;          // the finishing workgroup
 constexpr int kBlocks = 128;            // histogram / gather grid
 constexpr int kBT = 256;                // threads per grid block
 constexpr int kMaxK = MDX_SAMPLE_MAX_TOP_K;
+constexpr int kLB = 256;                // per-range selection blocks (small-k path)
+constexpr int kSmallK = 64;             // the small-k path serves top_k up to this
+constexpr int kRange = 1024;            // values of one block range (small-k path: V <= kLB * kRange)
 
 static_assert(kMaxK <= kThreads, "one candidate per thread in the ranking");
+static_assert(kSmallK == 64 && kLB % (kThreads / 64) == 0, "one list per wave, whole lists per wave");
 
 // Scratch in device memory, cleared by k_sample_clear at the start of a call.
 struct SampleScratch {
@@ -55,6 +64,9 @@ struct SampleScratch {
     int tiecount[kBlocks];      // keys equal to the threshold, per block range
     int cand_idx[kMaxK];
     float cand_val[kMaxK];
+    // small-k path: block b's 64 best candidates as ranking keys (rank_key),
+    // in ranking order; 0 fills the slots past its eligible values
+    unsigned long long loc_top[kLB][kSmallK];
 };
 
 // The reference's empty-slot value: only v > kFloor can become a candidate.
@@ -78,19 +90,15 @@ __device__ inline void block_range(int V, int b, int& r0, int& r1) {
     r1 = r0 + chunk < V ? r0 + chunk : V;
 }
 
-// The radix levels [0, levels) resolved from the histograms, by the 64 lanes
-// of one wave: the key prefix they fix and how many keys equal to the full
-// threshold are still needed.  At each level the digit d is the one whose
-// bin holds the need-th largest remaining key: above(d) < need <= above(d) +
-// hist[d], above(d) being the count in the bins above d (a suffix sum over
-// the lanes, four bins per lane).
-__device__ inline void resolve(const SampleScratch* sc, int levels, int k, uint32_t& prefix,
-                               uint32_t& need) {
+// One radix level resolved from its 256-bin histogram by the 64 lanes of one
+// wave: the digit d whose bin holds the need-th largest remaining key,
+// above(d) < need <= above(d) + hist[d], above(d) being the count in the bins
+// above d (a suffix sum over the lanes, four bins per lane); need drops by
+// above(d).  With fewer than need keys in all bins the digit is 0.
+__device__ inline uint32_t resolve_level(const uint32_t* hist, uint32_t& need) {
     const int lane = threadIdx.x & 63;
-    prefix = 0u;
-    need = (uint32_t)k;
-    for (int lv = 0; lv < levels; lv++) {
-        const uint4 h = *reinterpret_cast<const uint4*>(&sc->hist[lv][4 * lane]);
+    {
+        const uint4 h = *reinterpret_cast<const uint4*>(&hist[4 * lane]);
         const uint32_t loc = h.x + h.y + h.z + h.w;
         uint32_t incl = loc;                        // bins of lanes >= this one
         for (int off = 1; off < 64; off <<= 1) {
@@ -116,8 +124,310 @@ __device__ inline void resolve(const SampleScratch* sc, int levels, int k, uint3
             above = __shfl(at, src);
         }
         need -= above;
-        prefix |= (uint32_t)d << (24 - 8 * lv);
+        return (uint32_t)d;
     }
+}
+
+// The radix levels [0, levels) resolved from the histograms in scratch: the
+// key prefix they fix and how many keys equal to the full threshold are still
+// needed.
+__device__ inline void resolve(const SampleScratch* sc, int levels, int k, uint32_t& prefix,
+                               uint32_t& need) {
+    prefix = 0u;
+    need = (uint32_t)k;
+    for (int lv = 0; lv < levels; lv++) prefix |= resolve_level(sc->hist[lv], need) << (24 - 8 * lv);
+}
+
+// Ranking key of a candidate: its order key above the complemented index, so
+// that a descending order is (value desc, index asc).  Key 0 sorts last.
+__device__ inline unsigned long long rank_key(uint32_t key, int idx) {
+    return ((unsigned long long)key << 32) | (0xffffffffu - (uint32_t)idx);
+}
+__device__ inline int rank_index(unsigned long long rk) { return (int)(0xffffffffu - (uint32_t)rk); }
+
+// Descending bitonic sort of N (a power of two) keys in LDS, one per thread.
+template <int N>
+__device__ inline void bitonic_desc(unsigned long long* a, int tid) {
+    for (int size = 2; size <= N; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const int o = tid ^ stride;
+            if (tid < N && o > tid) {
+                const unsigned long long x = a[tid], y = a[o];
+                const bool desc = (tid & size) == 0;
+                if (desc ? x < y : x > y) {
+                    a[tid] = y;
+                    a[o] = x;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// The draw from k ranked candidates (sidx/sval by value desc, index asc;
+// empty slots (0, -1e30)): e_j = expf(v_j - v_0), running sums in rank order
+// (the reference's sequential float sum), the nucleus prefix and the draw as
+// the first crossing of a threshold, found in parallel (running sums of
+// non-negative terms never decrease, so each crossing is unique).  ebuf holds
+// k floats of workgroup scratch, 16-byte aligned, its length a multiple of 4.
+// Called by every thread of the workgroup.
+__device__ inline void finish(int k, const int* sidx, const float* sval, float* ebuf, float top_p,
+                              float u, int* out, int* top_idx, float* top_val) {
+    __shared__ __align__(16) float run[kMaxK];
+    __shared__ int s_m, s_pick;
+    const int tid = threadIdx.x;
+    if (tid < k) ebuf[tid] = expf(sval[tid] - sval[0]);
+    __syncthreads();
+    if (tid == 0) {
+        // one term after another (16-byte LDS reads and writes; the terms and
+        // sums past k are never read)
+        float acc = 0.0f;
+        for (int j = 0; j < k; j += 4) {
+            const float4 e = *reinterpret_cast<const float4*>(ebuf + j);
+            float4 r;
+            acc += e.x; r.x = acc;
+            acc += e.y; r.y = acc;
+            acc += e.z; r.z = acc;
+            acc += e.w; r.w = acc;
+            *reinterpret_cast<float4*>(run + j) = r;
+        }
+        s_m = k;
+    }
+    __syncthreads();
+    if (top_p < 1.0f && tid < k) {
+        const float lim = top_p * run[k - 1];
+        if (run[tid] >= lim && (tid == 0 || run[tid - 1] < lim)) s_m = tid + 1;
+    }
+    __syncthreads();
+    const int m = s_m;
+    if (tid == 0) s_pick = m - 1;       // no crossing (u = 1): the last kept
+    __syncthreads();
+    const float r = u * run[m - 1];
+    if (tid < m && r < run[tid] && (tid == 0 || !(r < run[tid - 1]))) s_pick = tid;
+    __syncthreads();
+    if (tid == 0) {
+        out[0] = sidx[s_pick];
+        out[1] = m;
+    }
+    if (top_idx && tid < k) top_idx[tid] = sidx[tid];
+    if (top_val && tid < k) top_val[tid] = sval[tid];
+}
+
+// Inclusive scan of one int per thread over a workgroup of NT threads: within
+// each wave by shuffles, then over the wave totals (wsum: NT/64 ints of LDS).
+// *total receives the workgroup's sum.
+template <int NT>
+__device__ inline int scan_incl(int* wsum, int v, int* total) {
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    if (wave == 0) {
+        int w = lane < NW ? wsum[lane] : 0;
+#pragma unroll
+        for (int off = 1; off < NW; off <<= 1) {
+            const int y = __shfl_up(w, off, 64);
+            if (lane >= off) w += y;
+        }
+        if (lane < NW) wsum[lane] = w;
+    }
+    __syncthreads();
+    const int r = x + (wave ? wsum[wave - 1] : 0);
+    *total = wsum[NW - 1];
+    __syncthreads();   // wsum is reused by the next scan
+    return r;
+}
+
+// ---- small-k path: wave-level bitonic top-64 ------------------------------
+//
+// A wave holds 64 ranking keys, one per lane.  wave_sort_desc sorts them in
+// descending order across the lanes (lane 0 the best); wave_merge_top keeps
+// the best 64 of two such sorted sets (the lane-wise maximum of one set and
+// the other reversed is bitonic and holds the best 64, which six merge steps
+// sort).  The ranking key is a total order, so the result is the exact top-64
+// of the values seen, in the reference's order (value desc, index asc).
+// Lane exchanges on the VALU: the value of lane l ^ J (DPP moves within a
+// 16-lane row, the gfx950 row swaps across rows), and of lane 63 - l.
+template <int CTRL>
+__device__ inline uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int J>
+__device__ inline uint32_t xor_lane(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (J == 1) return dpp_u32<0xB1>(v);            // quad_perm [1,0,3,2]
+    else if constexpr (J == 2) return dpp_u32<0x4E>(v);       // quad_perm [2,3,0,1]
+    else if constexpr (J == 4) {
+        const uint32_t up = dpp_u32<0x104>(v);                // row_shl:4: lane l + 4
+        const uint32_t dn = dpp_u32<0x114>(v);                // row_shr:4: lane l - 4
+        return (lane & 4) ? dn : up;
+    } else if constexpr (J == 8) return dpp_u32<0x128>(v);    // row_ror:8
+    else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+template <int J>
+__device__ inline unsigned long long xor_lane_u64(unsigned long long v) {
+    const uint32_t lo = xor_lane<J>((uint32_t)v), hi = xor_lane<J>((uint32_t)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ inline unsigned long long reverse_lanes_u64(unsigned long long v) {
+    // row_mirror (c -> 15 - c), then rows r -> r ^ 3
+    uint32_t lo = dpp_u32<0x140>((uint32_t)v), hi = dpp_u32<0x140>((uint32_t)(v >> 32));
+    lo = xor_lane<16>(xor_lane<32>(lo));
+    hi = xor_lane<16>(xor_lane<32>(hi));
+    return ((unsigned long long)hi << 32) | lo;
+}
+// One compare-exchange step at distance J: keep_max lanes keep the larger key.
+template <int J>
+__device__ inline unsigned long long cmpx(unsigned long long v, bool keep_max) {
+    const unsigned long long o = xor_lane_u64<J>(v);
+    return keep_max ? (v > o ? v : o) : (v < o ? v : o);
+}
+template <int SIZE, int J>
+__device__ inline unsigned long long sort_stage(unsigned long long v, int lane) {
+    if constexpr (J == 0) {
+        return v;
+    } else {
+        // the lower lane of a descending pair keeps the larger key
+        v = cmpx<J>(v, ((lane & J) == 0) == ((lane & SIZE) == 0));
+        return sort_stage<SIZE, J / 2>(v, lane);
+    }
+}
+template <int SIZE>
+__device__ inline unsigned long long sort_from(unsigned long long v, int lane) {
+    if constexpr (SIZE > 64) {
+        return v;
+    } else {
+        v = sort_stage<SIZE, SIZE / 2>(v, lane);
+        return sort_from<SIZE * 2>(v, lane);
+    }
+}
+__device__ inline unsigned long long wave_sort_desc(unsigned long long v) {
+    return sort_from<2>(v, threadIdx.x & 63);
+}
+template <int J>
+__device__ inline unsigned long long clean_desc(unsigned long long v, int lane) {
+    if constexpr (J == 0) {
+        return v;
+    } else {
+        v = cmpx<J>(v, (lane & J) == 0);
+        return clean_desc<J / 2>(v, lane);
+    }
+}
+__device__ inline unsigned long long wave_merge_top(unsigned long long a, unsigned long long b) {
+    const int lane = threadIdx.x & 63;
+    const unsigned long long rb = reverse_lanes_u64(b);
+    const unsigned long long v = a > rb ? a : rb;
+    return clean_desc<32>(v, lane);
+}
+// The best 64 of N sorted sets, merged as a tree: the merges of one level are
+// independent, so their instruction streams interleave.
+template <int N>
+__device__ inline unsigned long long tree_merge(unsigned long long (&x)[N]) {
+#pragma unroll
+    for (int step = 1; step < N; step *= 2)
+#pragma unroll
+        for (int i = 0; i + step < N; i += 2 * step) x[i] = wave_merge_top(x[i], x[i + step]);
+    return x[0];
+}
+
+// Small-k path, step 1: block b keeps the 64 best ranking keys of its
+// contiguous range (at most kRange values): each wave sorts its chunks of 64
+// and merges them, then wave 0 merges the four waves' sets.  The loops are
+// kept rolled: each sort or merge is one copy of straight-line code that
+// every iteration reuses (unrolled, the instruction fetch of code that runs
+// once per launch dominated the kernel).
+__global__ __launch_bounds__(kBT) void k_sample_local(const float* __restrict__ logits, int V, float temp,
+                                                      SampleScratch* sc) {
+    constexpr int NW = kBT / 64;
+    constexpr int PER = kRange / kBT;
+    __shared__ unsigned long long wl[NW][64];
+    __shared__ float vs[NW][PER][64];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int chunk = (V + kLB - 1) / kLB;
+    const int r0 = min(V, b * chunk), r1 = min(V, r0 + chunk);
+    const int n = r1 - r0;
+    // element 64 (wave + NW c) + lane of the range; every load issued first
+    float v[PER];
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+        const int i = 64 * (wave + NW * c) + lane;
+        v[c] = i < n ? logits[r0 + i] : 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < PER; c++) vs[wave][c][lane] = v[c];
+    unsigned long long top = 0ull;
+#pragma unroll 1
+    for (int c = 0; c < PER; c++) {
+        const int i = 64 * (wave + NW * c) + lane;
+        if (64 * (wave + NW * c) >= n) break;            // uniform over the wave
+        const uint32_t key = i < n ? order_key(tempered(vs[wave][c][lane], temp)) : 0u;
+        const unsigned long long x = wave_sort_desc(key ? rank_key(key, r0 + i) : 0ull);
+        top = c == 0 ? x : wave_merge_top(top, x);
+    }
+    wl[wave][lane] = top;
+    __syncthreads();
+    if (wave == 0) {
+        unsigned long long t = wl[0][lane];
+#pragma unroll 1
+        for (int w = 1; w < NW; w++) t = wave_merge_top(t, wl[w][lane]);
+        sc->loc_top[b][lane] = t;
+    }
+}
+
+// Small-k path, step 2: one workgroup merges the 256 block lists (each wave
+// 16 of them, then wave 0 the 16 results): the first k ranking keys are the
+// reference's k candidates in rank order.  Keys 0 (fewer than k eligible
+// values) are the empty slots (index 0, -1e30).
+__global__ __launch_bounds__(kThreads) void k_sample_merge(const float* __restrict__ logits, float temp,
+                                                           int k, float top_p, float u,
+                                                           const SampleScratch* sc, int* __restrict__ out,
+                                                           int* __restrict__ top_idx,
+                                                           float* __restrict__ top_val) {
+    constexpr int NW = kThreads / 64;
+    constexpr int BPW = kLB / NW;
+    __shared__ unsigned long long wl[NW][64];
+    __shared__ unsigned long long lists[NW][BPW][64];
+    __shared__ int sidx[kSmallK];
+    __shared__ float sval[kSmallK];
+    __shared__ __align__(16) float ebuf[kSmallK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        unsigned long long x[BPW];
+#pragma unroll
+        for (int q = 0; q < BPW; q++) x[q] = sc->loc_top[wave * BPW + q][lane];
+#pragma unroll
+        for (int q = 0; q < BPW; q++) lists[wave][q][lane] = x[q];
+    }
+    unsigned long long t = lists[wave][0][lane];
+#pragma unroll 1
+    for (int q = 1; q < BPW; q++) t = wave_merge_top(t, lists[wave][q][lane]);
+    wl[wave][lane] = t;
+    __syncthreads();
+    if (wave == 0) {
+        t = wl[0][lane];
+#pragma unroll 1
+        for (int w = 1; w < NW; w++) t = wave_merge_top(t, wl[w][lane]);
+        if (lane < k) {
+            const bool real = (t >> 32) != 0ull;
+            const int i = real ? rank_index(t) : 0;
+            sidx[lane] = i;
+            sval[lane] = real ? tempered(logits[i], temp) : kFloor;
+        }
+    }
+    __syncthreads();
+    finish(k, sidx, sval, ebuf, top_p, u, out, top_idx, top_val);
 }
 
 __global__ __launch_bounds__(256) void k_repeat_penalty(float* logits, const int* toks, int n,
@@ -203,20 +513,6 @@ __global__ __launch_bounds__(kBT) void k_sample_gather(const float* __restrict__
     if (tid == 0) sc->tiecount[blockIdx.x] = s_ties;
 }
 
-// Inclusive scan of one int per thread over the workgroup.
-__device__ inline int block_scan(int* buf, int v) {
-    const int tid = threadIdx.x;
-    buf[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < kThreads; off <<= 1) {
-        const int a = tid >= off ? buf[tid - off] : 0;
-        __syncthreads();
-        buf[tid] += a;
-        __syncthreads();
-    }
-    return buf[tid];
-}
-
 // The finishing workgroup: the candidates above the threshold, the first
 // `need` ties in index order (rescanning only the block ranges that hold
 // them), the ranking, softmax, top-p and the draw.
@@ -228,9 +524,10 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
                                                            float* __restrict__ top_val) {
     __shared__ uint32_t s_kstar;
     __shared__ int s_need;
-    __shared__ int scan[kThreads];
+    __shared__ int wsum[kThreads / 64];
     __shared__ int cidx[kMaxK], sidx[kMaxK];
-    __shared__ float cval[kMaxK], sval[kMaxK];
+    __shared__ __align__(16) float cval[kMaxK];
+    __shared__ float sval[kMaxK];
     const int tid = threadIdx.x;
     if (tid < 64) {
         uint32_t prefix, need;
@@ -264,74 +561,32 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(const float* __restri
                 v = tempered(logits[i], temp);
                 flag = order_key(v) == kstar;
             }
-            const int incl = block_scan(scan, flag);
+            int tot;
+            const int incl = scan_incl<kThreads>(wsum, flag, &tot);
             const int pos = base + incl - flag;
             if (flag && pos < need) {
                 cidx[greater + pos] = i;
                 cval[greater + pos] = v;
             }
-            base += scan[kThreads - 1];
-            __syncthreads();
+            base += tot;
         }
     }
     __syncthreads();
 
-    // rank by (value desc, index asc); the pairs are distinct, so the ranks
-    // are a permutation of 0..nc-1; the empty slots follow
-    __shared__ uint32_t ckey[kMaxK];
-    if (tid < nc) ckey[tid] = order_key(cval[tid]);
+    // rank by (value desc, index asc): a bitonic sort of 64-bit keys (the
+    // order key of the value above the complemented index; the pairs are
+    // distinct); the empty slots follow as (index 0, -1e30)
+    __shared__ unsigned long long sk[kThreads];
+    sk[tid] = tid < nc ? rank_key(order_key(cval[tid]), cidx[tid]) : 0ull;
     __syncthreads();
-    if (tid < nc) {
-        const uint32_t kj = ckey[tid];
-        const int ij = cidx[tid];
-        int r = 0;
-        for (int m = 0; m < nc; m++) {
-            const uint32_t km = ckey[m];
-            r += km > kj || (km == kj && cidx[m] < ij);
-        }
-        sidx[r] = ij;
-        sval[r] = cval[tid];
-    } else if (tid < k) {
-        sidx[tid] = 0;
-        sval[tid] = kFloor;
+    bitonic_desc<kThreads>(sk, tid);
+    if (tid < k) {
+        const int i = tid < nc ? rank_index(sk[tid]) : 0;
+        sidx[tid] = i;
+        sval[tid] = tid < nc ? tempered(logits[i], temp) : kFloor;
     }
     __syncthreads();
-
-    // softmax over the candidates: running sums in rank order (the
-    // reference's sequential float sum), then the nucleus prefix and the draw
-    // as the first crossing of a threshold, found in parallel (running sums
-    // of non-negative terms never decrease, so each crossing is unique)
-    __shared__ float run[kMaxK];
-    __shared__ int s_m, s_pick;
-    if (tid < k) cval[tid] = expf(sval[tid] - sval[0]);
-    __syncthreads();
-    if (tid == 0) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < k; j++) {
-            acc += cval[j];
-            run[j] = acc;
-        }
-        s_m = k;
-    }
-    __syncthreads();
-    if (top_p < 1.0f && tid < k) {
-        const float lim = top_p * run[k - 1];
-        if (run[tid] >= lim && (tid == 0 || run[tid - 1] < lim)) s_m = tid + 1;
-    }
-    __syncthreads();
-    const int m = s_m;
-    if (tid == 0) s_pick = m - 1;       // no crossing (u = 1): the last kept
-    __syncthreads();
-    const float r = u * run[m - 1];
-    if (tid < m && r < run[tid] && (tid == 0 || !(r < run[tid - 1]))) s_pick = tid;
-    __syncthreads();
-    if (tid == 0) {
-        out[0] = sidx[s_pick];
-        out[1] = m;
-    }
-    if (top_idx && tid < k) top_idx[tid] = sidx[tid];
-    if (top_val && tid < k) top_val[tid] = sval[tid];
+    finish(k, sidx, sval, cval, top_p, u, out, top_idx, top_val);
 }
 
 // The sampler scratch of mdx_sample_topk_noalloc, for callers that cannot
@@ -401,6 +656,12 @@ int mdx_launch_topk_sample(const float* logits, int V, float temperature, int k,
         return -1;
     hipStream_t s = (hipStream_t)stream;
     SampleScratch* sc = (SampleScratch*)scratch;
+    if (k <= kSmallK && V <= kLB * kRange) {
+        hipLaunchKernelGGL(k_sample_local, dim3(kLB), dim3(kBT), 0, s, logits, V, temperature, sc);
+        hipLaunchKernelGGL(k_sample_merge, dim3(1), dim3(kThreads), 0, s, logits, temperature, k, top_p,
+                           uniform, (const SampleScratch*)sc, out, top_idx, top_val);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     hipLaunchKernelGGL(k_sample_clear, dim3(1), dim3(256), 0, s, sc);
     for (int level = 0; level < 4; level++)
         hipLaunchKernelGGL(k_sample_hist, dim3(kBlocks), dim3(kBT), 0, s, logits, V, temperature, k,
