@@ -488,11 +488,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     }
 
     // lm_head rows of this workgroup; the first batch is requested during the
-    // last layer's gate/up stage
-#ifndef MDX_LM_ROWS
-#define MDX_LM_ROWS 16
-#endif
-    constexpr int U = MDX_LM_ROWS;      // rows per wave batch (power of two, <= 64)
+    // last layer's gate/up stage.  Rows per wave batch (power of two, <= 64):
+    // the first batch's registers are live through the whole layer loop (it
+    // is loaded inside the loop and used after it), and the kernel runs at
+    // the register limit, with AGPRs as spill space.  8-row batches free 32 of
+    // them: with fp16 layers 473.1 -> 471.3 us/token, int4 at KV 4096 580.1 ->
+    // 567.3; with int8 layers 16 and 8 measure the same (463), 4 is slower for
+    // fp16 and int4 (the lm_head keeps fewer bytes in flight).
+    constexpr int U = KIND == MDX_W_I8 ? 16 : 8;
     constexpr int PER = 64 / U;         // lanes holding one row's total
     const int rb = (int)(((long long)b * a.vocab) / NB);
     const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
