@@ -493,9 +493,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     // is loaded inside the loop and used after it), and the kernel runs at
     // the register limit, with AGPRs as spill space.  8-row batches free 32 of
     // them: with fp16 layers 473.1 -> 471.3 us/token, int4 at KV 4096 580.1 ->
-    // 567.3; with int8 layers 16 and 8 measure the same (463), 4 is slower for
-    // fp16 and int4 (the lm_head keeps fewer bytes in flight).
+    // 567.3 (4 is slower for both: the lm_head keeps fewer bytes in flight).
+    // With int8 layers the first batch of 16 rows goes straight to LDS instead
+    // (global_load_lds, no registers): 460.5 -> 456.4 us/token; the same for
+    // fp16 and int4 costs 1.5 and 2.5 us.
     constexpr int U = KIND == MDX_W_I8 ? 16 : 8;
+    constexpr bool kLmLds = KIND == MDX_W_I8;
     constexpr int PER = 64 / U;         // lanes holding one row's total
     const int rb = (int)(((long long)b * a.vocab) / NB);
     const int re = (int)(((long long)(b + 1) * a.vocab) / NB);
@@ -510,6 +513,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     };
     uint4 w0[U];
     float sc0 = 0.0f;
+    __shared__ uint4 lmb[kLmLds ? 4 : 1][kLmLds ? U : 1][64];   // [wave][row][lane]
 
     for (int l = 0; l < L; l++) {
         const mdx_persist_layer Ly = layer_at(a, l);
@@ -884,7 +888,20 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         // ================= E: RMSNorm + gate/up + SwiGLU ==========
         const bool last = l + 1 == L;
         if (!last) rm_load<KIND, 16, D>(wA, layer_at(a, l + 1).wqkv, rowA, t, 0, SA::NW);
-        else if (a.head) load_rows(w0, sc0, rb + wave * U);
+        else if (a.head) {
+            if constexpr (kLmLds) {
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int r = min(rb + wave * U + u, re - 1);
+                    __builtin_amdgcn_global_load_lds(a.lm_w + (size_t)r * D + lane * 16,
+                                                     (__attribute__((address_space(3))) void*)&lmb[wave][u][0],
+                                                     16, 0, 0);
+                }
+                sc0 = a.lm_scale[min(rb + wave * U + lane / PER, re - 1)];
+            } else {
+                load_rows(w0, sc0, rb + wave * U);
+            }
+        }
         const float4 nwE = reinterpret_cast<const float4*>(Ly.post_norm)[t];
         const float sclE = Ly.sgu ? Ly.sgu[rowE(t < 24 ? t : 0)] : 1.0f;
         {
@@ -989,6 +1006,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             if (__syncthreads_or(!ok)) dead = true;
         }
         MDX_TRACE(16 * L + 0);
+        if constexpr (kLmLds) {
+            // this wave's loads complete in order, so its LDS batch landed
+            // before the h words it has just read
+#pragma unroll
+            for (int u = 0; u < U; u++) w0[u] = lmb[wave][u][lane];
+        }
         {
             const float tot = (ws[0] + ws[1]) + (ws[2] + ws[3]);
             const float rms = 1.0f / sqrtf(tot / (float)D + a.eps);
