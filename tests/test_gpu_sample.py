@@ -48,8 +48,10 @@ def _check(mdx, oracle_lib, x, **kw):
     return tok
 
 
-@pytest.mark.parametrize("k", [1, 2, 40, 1000, 1024])
+@pytest.mark.parametrize("k", [1, 2, 40, 64, 65, 1000, 1024])
 def test_top_k_full_vocab(mdx, gpu, oracle_lib, k):
+    # k <= 64 runs the two-launch path (per-range top-64 lists, one merging
+    # workgroup), k >= 65 the radix-select path: both sides of the switch
     x = _logits(V_FULL, 100 + k)
     for u in (0.0, 0.37, 0.999):
         tok = _check(mdx, oracle_lib, x, top_k=k, u=u)
@@ -77,13 +79,15 @@ def test_repeat_penalty(mdx, gpu, oracle_lib):
     assert tok == oracle_lib.sample_topk(x, top_k=1, repeat_tokens=toks, repeat_penalty=5.0)[0]
 
 
-@pytest.mark.parametrize("V", [V_FULL, 151669, 1001, 5])
+@pytest.mark.parametrize("V", [V_FULL, 151669, 1001, 5, 300001])
 def test_ties_signed_zeros_and_ragged_vocab(mdx, gpu, oracle_lib, V):
+    # 300001 values exceed what the two-launch small-k path covers (256
+    # ranges of at most 1024), so every k there takes the radix-select path
     # values on a coarse grid: long runs of equal values at the threshold, and
     # both +0 and -0 (np.round keeps the sign)
     x = _logits(V, V, scale=1.0, quant=2)
     assert np.any(np.signbit(x) & (x == 0)) or V < 100
-    for k in sorted({1, 3, min(V, 257), min(V, 1024)}):
+    for k in sorted({1, 3, min(V, 64), min(V, 257), min(V, 1024)}):
         _check(mdx, oracle_lib, x, top_k=k, u=0.6)
     # every value equal: the first k indices
     z = np.zeros(V, np.float32)
