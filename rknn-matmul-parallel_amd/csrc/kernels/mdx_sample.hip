@@ -3,8 +3,9 @@
 // the host.  For top_k <= 64 (the usual sampling settings) two launches:
 // 256 workgroups each keep the 64 best of their contiguous index range as
 // 64-bit ranking keys, sorted with wave-level bitonic networks in registers;
-// one workgroup of 1024 threads merges the 256 lists the same way, and the
-// first k keys are the candidates in rank order.  Larger k: seven short
+// 16 workgroups merge 16 lists each the same way, and the last of them to
+// finish merges their 16 results: the first k keys are the candidates in rank
+// order.  Larger k: seven short
 // launches, a scratch clear, four radix-select levels and a gather over 128
 // workgroups (each owns a contiguous index range), and one finishing
 // workgroup that ranks the candidates with a bitonic sort in LDS.
@@ -54,7 +55,7 @@ constexpr int kSmallK = 64;             // the small-k path serves top_k up to t
 constexpr int kRange = 1024;            // values of one block range (small-k path: V <= kLB * kRange)
 
 static_assert(kMaxK <= kThreads, "one candidate per thread in the ranking");
-static_assert(kSmallK == 64 && kLB % (kThreads / 64) == 0, "one list per wave, whole lists per wave");
+static_assert(kSmallK == 64 && kLB == 16 * 16, "16 merging workgroups of 16 lists");
 
 // Scratch in device memory, cleared by k_sample_clear at the start of a call.
 struct SampleScratch {
@@ -67,6 +68,8 @@ struct SampleScratch {
     // small-k path: block b's 64 best candidates as ranking keys (rank_key),
     // in ranking order; 0 fills the slots past its eligible values
     unsigned long long loc_top[kLB][kSmallK];
+    unsigned long long grp_top[kLB / 16][kSmallK];   // merged lists of 16 ranges each
+    unsigned merge_arrived;                           // zero between calls
 };
 
 // The reference's empty-slot value: only v > kFloor can become a candidate.
@@ -355,6 +358,7 @@ __global__ __launch_bounds__(kBT) void k_sample_local(const float* __restrict__ 
     __shared__ unsigned long long wl[NW][64];
     __shared__ float vs[NW][PER][64];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (b == 0 && tid == 0) sc->merge_arrived = 0u;   // the merge launch that follows counts from zero
     const int chunk = (V + kLB - 1) / kLB;
     const int r0 = min(V, b * chunk), r1 = min(V, r0 + chunk);
     const int n = r1 - r0;
@@ -386,45 +390,62 @@ __global__ __launch_bounds__(kBT) void k_sample_local(const float* __restrict__ 
     }
 }
 
-// Small-k path, step 2: one workgroup merges the 256 block lists (each wave
-// 16 of them, then wave 0 the 16 results): the first k ranking keys are the
-// reference's k candidates in rank order.  Keys 0 (fewer than k eligible
-// values) are the empty slots (index 0, -1e30).
+// Small-k path, step 2: 16 workgroups of 16 waves each merge 16 of the 256
+// range lists as a tree across their waves (four levels through LDS), store
+// the result and count their arrival; the last to arrive merges the 16
+// results the same way.  Its first k ranking keys are the reference's k
+// candidates in rank order; keys 0 (fewer than k eligible values) are the
+// empty slots (index 0, -1e30).
+constexpr int kMergeBlocks = kLB / 16;
+
+// The best 64 of the 16 waves' sets by a tree through LDS: on return wave 0
+// holds them.  set: 16 x 64 keys of LDS.
+__device__ inline unsigned long long tree_across_waves(unsigned long long t, unsigned long long (*set)[64]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int step = 1; step < 16; step *= 2) {
+        if (wave % (2 * step) == step) set[wave][lane] = t;
+        __syncthreads();
+        if (wave % (2 * step) == 0) t = wave_merge_top(t, set[wave + step][lane]);
+        __syncthreads();
+    }
+    return t;
+}
+
 __global__ __launch_bounds__(kThreads) void k_sample_merge(const float* __restrict__ logits, float temp,
                                                            int k, float top_p, float u,
-                                                           const SampleScratch* sc, int* __restrict__ out,
+                                                           SampleScratch* sc, int* __restrict__ out,
                                                            int* __restrict__ top_idx,
                                                            float* __restrict__ top_val) {
-    constexpr int NW = kThreads / 64;
-    constexpr int BPW = kLB / NW;
-    __shared__ unsigned long long wl[NW][64];
-    __shared__ unsigned long long lists[NW][BPW][64];
+    static_assert(kThreads == 16 * 64, "one list per wave");
+    __shared__ unsigned long long set[16][64];
+    __shared__ int s_last;
     __shared__ int sidx[kSmallK];
     __shared__ float sval[kSmallK];
     __shared__ __align__(16) float ebuf[kSmallK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    {
-        unsigned long long x[BPW];
-#pragma unroll
-        for (int q = 0; q < BPW; q++) x[q] = sc->loc_top[wave * BPW + q][lane];
-#pragma unroll
-        for (int q = 0; q < BPW; q++) lists[wave][q][lane] = x[q];
-    }
-    unsigned long long t = lists[wave][0][lane];
-#pragma unroll 1
-    for (int q = 1; q < BPW; q++) t = wave_merge_top(t, lists[wave][q][lane]);
-    wl[wave][lane] = t;
+    const int g = blockIdx.x;
+    unsigned long long t = tree_across_waves(sc->loc_top[16 * g + wave][lane], set);
+    // the result goes out with device-scope stores that complete before the
+    // arrival is counted, and the last block reads with device-scope loads:
+    // no cache write-back or invalidate is needed (a __threadfence pair here,
+    // which writes back the whole L2 of the XCD, took the kernel to 16.5 us)
+    if (wave == 0) __hip_atomic_store(&sc->grp_top[g][lane], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (wave == 0) {
-        t = wl[0][lane];
-#pragma unroll 1
-        for (int w = 1; w < NW; w++) t = wave_merge_top(t, wl[w][lane]);
-        if (lane < k) {
-            const bool real = (t >> 32) != 0ull;
-            const int i = real ? rank_index(t) : 0;
-            sidx[lane] = i;
-            sval[lane] = real ? tempered(logits[i], temp) : kFloor;
-        }
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&sc->merge_arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(kMergeBlocks - 1);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(&sc->merge_arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t = tree_across_waves(__hip_atomic_load(&sc->grp_top[wave][lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                          set);
+    if (wave == 0 && lane < k) {
+        const bool real = (t >> 32) != 0ull;
+        const int i = real ? rank_index(t) : 0;
+        sidx[lane] = i;
+        sval[lane] = real ? tempered(logits[i], temp) : kFloor;
     }
     __syncthreads();
     finish(k, sidx, sval, ebuf, top_p, u, out, top_idx, top_val);
@@ -658,8 +679,8 @@ int mdx_launch_topk_sample(const float* logits, int V, float temperature, int k,
     SampleScratch* sc = (SampleScratch*)scratch;
     if (k <= kSmallK && V <= kLB * kRange) {
         hipLaunchKernelGGL(k_sample_local, dim3(kLB), dim3(kBT), 0, s, logits, V, temperature, sc);
-        hipLaunchKernelGGL(k_sample_merge, dim3(1), dim3(kThreads), 0, s, logits, temperature, k, top_p,
-                           uniform, (const SampleScratch*)sc, out, top_idx, top_val);
+        hipLaunchKernelGGL(k_sample_merge, dim3(kMergeBlocks), dim3(kThreads), 0, s, logits, temperature, k,
+                           top_p, uniform, sc, out, top_idx, top_val);
         return hipGetLastError() == hipSuccess ? 0 : -4;
     }
     hipLaunchKernelGGL(k_sample_clear, dim3(1), dim3(256), 0, s, sc);
