@@ -285,14 +285,15 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         if (tid == 0) {
             unsigned long long b = bkey[0];
             for (int w = 1; w < 4; w++) b = bkey[w] > b ? bkey[w] : b;
-            if (b) atomicMax(a.amax_key, b);
-            __threadfence();
-            const unsigned prev = atomicAdd(a.done, 1u);
+            // device-scope atomics throughout, the maximum completed before
+            // the arrival is counted: no cache write-back is needed
+            if (b) __hip_atomic_fetch_max(a.amax_key, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            const unsigned prev = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             last_block = prev == gridDim.x - 1;
         }
         __syncthreads();
         if (last_block && tid == 0) {
-            __threadfence();
             const unsigned long long k = atomicExch(a.amax_key, 0ull);
             atomicExch(a.done, 0u);
             const int tok = ref_argmax_index(k);
@@ -385,20 +386,20 @@ __global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
     if (tid == 0) {
         unsigned long long bk = bkey[0];
         for (int w = 1; w < 4; w++) bk = bkey[w] > bk ? bkey[w] : bk;
-        keys[blockIdx.x] = bk;
-        __threadfence();
+        // the key goes out with a device-scope store that completes before
+        // the arrival is counted, and the last block reads the keys with
+        // device-scope loads: no cache write-back or invalidate is needed
+        __hip_atomic_store(&keys[blockIdx.x], bk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
         const int grp = blockIdx.x % kLmGroups;
         const unsigned in_grp = (gridDim.x - grp + kLmGroups - 1) / kLmGroups;
         int last = 0;
-        if (atomicAdd(&cnt[grp], 1u) == in_grp - 1) {
-            __threadfence();
-            last = atomicAdd(top, 1u) == kLmGroups - 1;
-        }
+        if (__hip_atomic_fetch_add(&cnt[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_grp - 1)
+            last = __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kLmGroups - 1;
         last_block = last;
     }
     __syncthreads();
     if (last_block) {
-        __threadfence();
         unsigned long long k = 0ull;
         for (int i = tid; i < (int)gridDim.x; i += 256) {
             const unsigned long long v = __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -413,12 +414,12 @@ __global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
         }
         if (lane == 0) bkey[wave] = k;
         __syncthreads();
-        if (tid < kLmGroups) cnt[tid] = 0u;
+        if (tid < kLmGroups) __hip_atomic_store(&cnt[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (last_block && tid == 0) {
         unsigned long long k = bkey[0];
         for (int w = 1; w < 4; w++) k = bkey[w] > k ? bkey[w] : k;
-        *top = 0u;
+        __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int tok = ref_argmax_index(k);
         mdx_state* st = a.st;
         st->argmax = tok;
