@@ -710,7 +710,8 @@ static void setup_persist(MatmulDecoderContext* c) {
     c->persist = 1;
 }
 
-static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
+/* pos: the position the launch processes (it attends over pos + 1) */
+static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens, int pos) {
     if (head && !c->persist_head) return MATMUL_DECODER_ERR_INVALID_ARG;
     c->pargs.head = head;
     c->pargs.advance = 1;
@@ -721,8 +722,9 @@ static int launch_persist(MatmulDecoderContext* c, int head, int* out_tokens) {
     /* K/V rows of a long context are streamed past the last-level cache
      * (256 MB), which then keeps the 156 MB INT8 lm_head from step to step;
      * a short context's rows (read again every step) stay cached */
-    const double kv_bytes = 2.0 * c->L * (double)(c->seq_len + 1) * c->kvd * 2.0;
+    const double kv_bytes = 2.0 * c->L * (double)(pos + 1) * c->kvd * 2.0;
     c->pargs.kv_stream = c->kv_stream_force >= 0 ? c->kv_stream_force : kv_bytes > 96.0 * 1024 * 1024;
+    c->pargs.k_passes = mdx_persist_k_passes(pos + 1);
     return mdx_launch_persist_step(&c->pargs, c->stream);
 }
 
@@ -1122,12 +1124,12 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     if (!rc && prof) rc = trace_arm(c);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
     if (c->persist && (c->persist_head || !want_head)) {
-        if (!rc) rc = launch_persist(c, want_head, NULL);
+        if (!rc) rc = launch_persist(c, want_head, NULL, c->seq_len);
         if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     } else if (c->persist) {
         /* the fp16 lm_head: layers in one launch (which advances the
          * position), then the per-stage head */
-        if (!rc) rc = launch_persist(c, 0, NULL);
+        if (!rc) rc = launch_persist(c, 0, NULL, c->seq_len);
         if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
         if (!rc) rc = run_head(c, &c->lm, NULL, 0, c->stream);
     } else {
@@ -1219,7 +1221,7 @@ int matmul_decoder_step_head(MatmulDecoderContext* c, int token_id, const float*
     rc = set_state(c, token_id, embedding);
     if (c->persist) {
         /* the one launch advances the position; the head does not */
-        if (!rc) rc = launch_persist(c, 0, NULL);
+        if (!rc) rc = launch_persist(c, 0, NULL, c->seq_len);
         if (!rc) rc = run_head(c, &c->lm_heads[lm_head_idx], NULL, 0, c->stream);
     } else {
         if (!rc) rc = launch_seq(c, c->g_layers, seq_layers);
@@ -1462,9 +1464,9 @@ int mdx_generate_greedy(MatmulDecoderContext* c, int first_token, int n_steps, i
         if (!c->persist) {
             rc = launch_seq(c, c->g_greedy, seq_greedy);
         } else if (c->persist_head) {
-            rc = launch_persist(c, 1, c->d_tokens);
+            rc = launch_persist(c, 1, c->d_tokens, c->seq_len + i);
         } else {
-            rc = launch_persist(c, 0, NULL);
+            rc = launch_persist(c, 0, NULL, c->seq_len + i);
             if (!rc) rc = run_head(c, &c->lm, c->d_tokens, 0, c->stream);
         }
     }
@@ -1635,7 +1637,7 @@ int mdx_trace_step(MatmulDecoderContext* c, int token_id, unsigned long long* ou
     if (!rc) rc = mdxrt_fill_u32(d, 0u, (size_t)256 * ev * 2, c->stream);
     c->pargs.trace = d;
     c->pargs.trace_stride = ev;
-    if (!rc) rc = launch_persist(c, 1, NULL);
+    if (!rc) rc = launch_persist(c, 1, NULL, c->seq_len);
     c->pargs.trace = NULL;
     c->pargs.trace_stride = 0;
     if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);

@@ -175,6 +175,9 @@ typedef struct {
     int kv_stream;                     /* 1: read the K/V rows with non-temporal loads (a
                                           cache too large to stay in the last-level cache
                                           next to the lm_head) */
+    int k_passes;                      /* 16-position K/V passes per round, 4 or 5: see
+                                          mdx_persist_k_passes (int8 and int4 layers; fp16
+                                          layers always take 4) */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */
@@ -182,6 +185,11 @@ int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F);
 /* 1 when the current device can hold the whole grid co-resident. */
 int mdx_persist_usable(int kind);
 size_t mdx_persist_xbuf_bytes(void);
+/* K/V passes per round for a step that attends over n_pos positions: 5 when
+ * rounds of 64 positions per split would take three or more rounds and rounds
+ * of 80 take fewer (the first two rounds are requested together; each later
+ * one is a dependent load round trip), else 4. */
+int mdx_persist_k_passes(int n_pos);
 /* Events per workgroup of a traced step: 16 per layer (stage starts, waits
  * done, outputs written), 3 for the lm_head and the workgroup's XCD index. */
 int mdx_persist_trace_events(int n_layers);

@@ -47,7 +47,6 @@ constexpr int NT = 256;                 // threads per workgroup
 constexpr int D = 1024, NQ = 16, NKV = 8, HD = 128, FF = 3072;
 constexpr int QD = NQ * HD, KVD = NKV * HD;
 constexpr int GRP = NB / NKV;           // workgroups per KV head
-constexpr int PP = 4;                   // 16-position K/V passes requested ahead
 constexpr unsigned kSpinLimit = 1u << 18;   // polling rounds before a wait gives up
 
 // exchange buffer layout, in 32-bit words
@@ -422,7 +421,13 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 
 // ---- the step kernel --------------------------------------------------------
 
-template <int KIND>
+// PP: 16-position K/V passes per round (a round's rows are requested
+// together).  4, or 5 for a context whose splits hold 129..160 positions (a
+// little over 4096): two rounds of 80 then replace a third dependent round
+// for the last few positions (W4A16 at KV 4096: 576 -> 558 us/token).  At
+// short contexts 5 passes cost 10 us (int8 at KV 512), so the host picks per
+// launch.
+template <int KIND, int PP>
 __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     using SA = RowMajor<KIND, 16, D>;       // qkv
     using SE = RowMajor<KIND, 24, D>;       // gate/up
@@ -1131,13 +1136,29 @@ __global__ __launch_bounds__(256) void k_persist_poison(unsigned* xb, int L) {
 
 typedef void (*PersistKernel)(PArgs);
 
-PersistKernel pick(int kind) {
+// fp16 weights leave no registers for the second K/V register set, so their
+// rounds run one at a time and keep 4 passes
+PersistKernel pick(int kind, int pass5) {
     switch (kind) {
-        case MDX_W_F16: return k_persist_step<MDX_W_F16>;
-        case MDX_W_I8: return k_persist_step<MDX_W_I8>;
-        case MDX_W_I4: return k_persist_step<MDX_W_I4>;
+        case MDX_W_F16: return k_persist_step<MDX_W_F16, 4>;
+        case MDX_W_I8: return pass5 ? k_persist_step<MDX_W_I8, 5> : k_persist_step<MDX_W_I8, 4>;
+        case MDX_W_I4: return pass5 ? k_persist_step<MDX_W_I4, 5> : k_persist_step<MDX_W_I4, 4>;
         default: return nullptr;
     }
+}
+
+// 1 when the device can hold k's whole grid co-resident
+int persist_fits(PersistKernel k) {
+    if (!k) return 0;
+    int dev = 0, coop = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop)
+        return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), NT, 0) !=
+        hipSuccess)
+        return 0;
+    return (long)per_cu * cus >= NB;
 }
 
 }  // namespace
@@ -1153,17 +1174,18 @@ int mdx_persist_shape_ok(int d, int nq, int nkv, int hd, int F) {
 size_t mdx_persist_xbuf_bytes(void) { return (size_t)W_TOTAL * 4; }
 
 int mdx_persist_usable(int kind) {
-    PersistKernel k = pick(kind);
-    if (!k) return 0;
-    int dev = 0, coop = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop)
-        return 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), NT, 0) !=
-        hipSuccess)
-        return 0;
-    return (long)per_cu * cus >= NB;
+    for (int pass5 = 0; pass5 < 2; pass5++)
+        if (!persist_fits(pick(kind, pass5))) return 0;
+    return 1;
+}
+
+int mdx_persist_k_passes(int n_pos) {
+    // positions per split, then rounds of 64 against rounds of 80; the first
+    // two rounds are requested before any is computed, so only a third or
+    // later round costs a dependent round trip
+    const int per = (n_pos + GRP - 1) / GRP;
+    const int r4 = (per + 63) / 64, r5 = (per + 79) / 80;
+    return r4 >= 3 && r5 < r4 ? 5 : 4;
 }
 
 int mdx_persist_debug_poison(void* xbuf, int n_layers, void* stream) {
@@ -1174,7 +1196,7 @@ int mdx_persist_debug_poison(void* xbuf, int n_layers, void* stream) {
 }
 
 int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
-    PersistKernel k = pick(p->kind);
+    PersistKernel k = pick(p->kind, p->k_passes == 5);
     if (!k || p->n_layers <= 0 || !p->state || !p->xbuf || !p->l0.wqkv) return -1;
     if (p->head && (!p->lm_w || !p->lm_scale || !p->logits || !p->final_norm)) return -1;
     PArgs a;

@@ -10,7 +10,9 @@ context creation):
 - the K/V row appended at the step's position;
 - cache lengths that exercise every attention chunking case: 0 (only the new
   position), 1, 33, 511, 600, 2100 (chunks longer than the 64 prefetched
-  positions) and 4100;
+  positions) and 4100 (129 positions per split: with int8 and int4 layers
+  the launch takes rounds of 80 positions), and 6200 for int8 and int4
+  (194 per split: three rounds of 80);
 - an uploaded embedding instead of a token, a step without the lm_head, and
   16 greedy steps fed back on the device.
 """
@@ -45,27 +47,28 @@ def models(mdx, workdir):
     return cfg, get
 
 
-def _pair(mdx, oracle_lib, cfg, path, quant, persist=True, shape=SHAPE, want_path=1):
+def _pair(mdx, oracle_lib, cfg, path, quant, persist=True, shape=SHAPE, want_path=1, max_seq=MAX_SEQ):
     old = os.environ.get("MDX_PERSIST")
     os.environ["MDX_PERSIST"] = "1" if persist else "0"
     try:
-        g = mdx.Decoder(path, cfg, QUANTS[quant], MAX_SEQ)
+        g = mdx.Decoder(path, cfg, QUANTS[quant], max_seq)
     finally:
         if old is None:
             del os.environ["MDX_PERSIST"]
         else:
             os.environ["MDX_PERSIST"] = old
     assert g.path == (want_path if persist else 0)
-    o = oracle_lib.Model(path, shape, quant, MAX_SEQ, kv_fp16=True)
+    o = oracle_lib.Model(path, shape, quant, max_seq, kv_fp16=True)
     return g, o
 
 
-@pytest.mark.parametrize("quant", [0, 1, 2])
-@pytest.mark.parametrize("n_pos", [0, 1, 33, 511, 600, 2100, 4100])
+@pytest.mark.parametrize("quant,n_pos", [(q, n) for q in (0, 1, 2)
+                                          for n in (0, 1, 33, 511, 600, 2100, 4100)]
+                         + [(1, 6200), (2, 6200)])
 def test_step_matches_oracle(mdx, gpu, oracle_lib, models, quant, n_pos):
     cfg, get = models
     path = get(quant)
-    g, o = _pair(mdx, oracle_lib, cfg, path, quant)
+    g, o = _pair(mdx, oracle_lib, cfg, path, quant, max_seq=max(MAX_SEQ, n_pos + 8))
     seed = 77 + n_pos
     if n_pos:
         g.kv_fill_normal(n_pos, seed)
