@@ -576,7 +576,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 }
             }
         };
-        load_kv(kr, vr, 0);
+        // the first K/V round: for int8 and int4 layers after the qkv GEMV
+        // (below), which otherwise waits for part of it (W4A16 at KV 4096
+        // 561.5 -> 556 us/token, int8 at KV 512 unchanged); fp16 layers here
+        // (after the GEMV: +11.5 us at KV 512)
+        constexpr bool kLateKV = KIND != MDX_W_F16;
+        if constexpr (!kLateKV) load_kv(kr, vr, 0);
         uint4 wD[SD::NW];
         cm_load<KIND, 4, QD>(wD, Ly.wo, 4 * b, t);
         MDX_TRACE(16 * l + 1);
@@ -588,6 +593,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         rm_dot<KIND, 16, D>(wA, xs4, red, t);
+        if constexpr (kLateKV) load_kv(kr, vr, 0);
         __syncthreads();
         if (wave == 0) {
             // lanes 0..15 hold rows s*16 + lane; even lanes store two rows in one

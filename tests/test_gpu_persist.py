@@ -11,8 +11,11 @@ context creation):
 - cache lengths that exercise every attention chunking case: 0 (only the new
   position), 1, 33, 511, 600, 2100 (chunks longer than the 64 prefetched
   positions) and 4100 (129 positions per split: with int8 and int4 layers
-  the launch takes rounds of 80 positions), and 6200 for int8 and int4
-  (194 per split: three rounds of 80);
+  the launch takes rounds of 80 positions), and for int4 and int8 layers
+  4095 and 4096 (128 and 129 per split, either side of the switch to
+  rounds of 80), 5500 (172 per split: three rounds of 64, the third
+  requested while the first is computed) and 6200 (194 per split: three
+  rounds of 80);
 - an uploaded embedding instead of a token, a step without the lm_head, and
   16 greedy steps fed back on the device.
 """
@@ -64,7 +67,7 @@ def _pair(mdx, oracle_lib, cfg, path, quant, persist=True, shape=SHAPE, want_pat
 
 @pytest.mark.parametrize("quant,n_pos", [(q, n) for q in (0, 1, 2)
                                           for n in (0, 1, 33, 511, 600, 2100, 4100)]
-                         + [(1, 6200), (2, 6200)])
+                         + [(2, 4095), (2, 4096), (1, 5500), (2, 5500), (1, 6200), (2, 6200)])
 def test_step_matches_oracle(mdx, gpu, oracle_lib, models, quant, n_pos):
     cfg, get = models
     path = get(quant)
