@@ -80,6 +80,7 @@ struct MatmulDecoderContext {
     mdx_state* h_state;
     float* h_io;
     int* h_samp;                 /* pinned: sampler tokens, then {token, kept} */
+    int* h_res;                  /* pinned: a host-fed step's {argmax, timeout flag} */
     size_t h_io_floats;
     void *ev0, *ev1, *ev2;
     MatmulDecoderStats stats;
@@ -893,6 +894,7 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
     if ((size_t)c->max_m * c->d > c->h_io_floats) c->h_io_floats = (size_t)c->max_m * c->d;
     if (mdxrt_host_alloc((void**)&c->h_io, c->h_io_floats * 4)) goto fail;
     if (mdxrt_host_alloc((void**)&c->h_samp, (MDX_SAMPLE_MAX_REPEAT + 64) * sizeof(int))) goto fail;
+    if (mdxrt_host_alloc((void**)&c->h_res, 4 * sizeof(int))) goto fail;
     memset(c->h_state, 0, sizeof(mdx_state));
     setup_persist(c);
     {
@@ -989,6 +991,7 @@ void matmul_decoder_destroy(MatmulDecoderContext* c) {
     mdxrt_host_free(c->h_state);
     mdxrt_host_free(c->h_io);
     mdxrt_host_free(c->h_samp);
+    mdxrt_host_free(c->h_res);
     mdxrt_event_destroy(c->ev0);
     mdxrt_event_destroy(c->ev1);
     mdxrt_event_destroy(c->ev2);
@@ -1119,8 +1122,30 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     }
     const int prof = c->profile && c->persist && c->d_trace;
     const int one_launch_head = c->persist && c->persist_head && want_head;
+    /* A plain step with the head in the one launch is host-fed: the position,
+     * token and mode go in as kernel arguments, and the kernel writes the
+     * argmax, the timeout flag and the logits to mapped host memory, so no
+     * copy runs before or after it.  Sampling and profiling steps, which read
+     * the device logits or the trace, keep the copies. */
+    const int host_fed = one_launch_head && !sr && !prof && (long long)c->V <= 256LL * 1024;
     if (c->persist) pthread_mutex_lock(&g_persist_mu);
-    rc = set_state(c, token_id, embedding);
+    if (host_fed) {
+        c->h_res[0] = -1;
+        c->h_res[1] = 0;
+        c->pargs.in_args = 1;
+        c->pargs.in_pos = c->seq_len;
+        c->pargs.in_token = embedding ? 0 : token_id;
+        c->pargs.in_mode = embedding ? 1 : 0;
+        c->pargs.res_host = c->h_res;
+        c->pargs.logits_host = output_logits ? c->h_io : NULL;
+        rc = 0;
+        if (embedding) {
+            memcpy(c->h_io, embedding, (size_t)c->d * 4);
+            rc = mdxrt_h2d_async(c->d_emb_in, c->h_io, (size_t)c->d * 4, c->stream);
+        }
+    } else {
+        rc = set_state(c, token_id, embedding);
+    }
     if (!rc && prof) rc = trace_arm(c);
     if (!rc) rc = mdxrt_event_record(c->ev0, c->stream);
     if (c->persist && (c->persist_head || !want_head)) {
@@ -1138,7 +1163,8 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
         if (!rc) rc = launch_seq(c, want_head ? c->g_head : c->g_adv, want_head ? seq_head : seq_adv);
     }
     if (!rc) rc = mdxrt_event_record(c->ev2, c->stream);
-    if (!rc && output_logits) rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
+    if (!rc && output_logits && !host_fed)
+        rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
     if (!rc && sr) {
         /* penalty and draw on the logits just copied out; the kernels read
          * the tokens from and write {token, kept} to pinned host memory */
@@ -1149,12 +1175,19 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
                                         c->d_sscr, c->h_samp + MDX_SAMPLE_MAX_REPEAT, NULL, NULL,
                                         c->stream);
     }
-    if (!rc) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
+    if (!rc && !host_fed) rc = mdxrt_d2h_async(c->h_state, c->d_state, sizeof(mdx_state), c->stream);
     if (!rc && prof)
         rc = mdxrt_d2h_async(c->h_trace, c->d_trace, (size_t)256 * c->trace_ev * 8, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
     c->pargs.trace = NULL;
     c->pargs.trace_stride = 0;
+    c->pargs.in_args = 0;
+    c->pargs.res_host = NULL;
+    c->pargs.logits_host = NULL;
+    if (host_fed && !rc) {
+        c->h_state->pad[1] = c->h_res[1];
+        c->h_state->argmax = c->h_res[0];
+    }
     if (c->persist) pthread_mutex_unlock(&g_persist_mu);
     if (rc) {
         fprintf(stderr, "[MatmulDecoder] step failed: %s\n", mdxrt_last_error());

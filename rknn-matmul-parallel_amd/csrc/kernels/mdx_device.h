@@ -178,6 +178,15 @@ typedef struct {
     int k_passes;                      /* 16-position K/V passes per round, 4 or 5: see
                                           mdx_persist_k_passes (int8 and int4 layers; fp16
                                           layers always take 4) */
+    int in_args;                       /* 1: the step's position, token and mode come from
+                                          the three fields below instead of the device
+                                          state (which the step still updates) */
+    int in_pos, in_token, in_mode;
+    float* logits_host;                /* optional (head only, vocab <= 256 * 1024): the
+                                          logits written to this mapped host buffer instead
+                                          of logits */
+    int* res_host;                     /* optional mapped host words: [0] <- the argmax,
+                                          [1] <- 1 when a wait timed out */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */

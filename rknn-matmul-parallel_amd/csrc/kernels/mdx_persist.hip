@@ -99,7 +99,15 @@ struct PArgs {
     int trace_stride;
     unsigned spin_limit;
     int kv_stream;
+    int in_args;                // 1: pos, token, mode from the three fields below, not st
+    int in_pos, in_token, in_mode;
+    float* logits_host;         // optional mapped host buffer for the logits (instead of logits)
+    int* res_host;              // optional mapped host words: [0] the argmax, [1] set on a timeout
 };
+
+// Rows of the lm_head per workgroup that the host-logits mode stages in LDS
+// (vocabularies up to 256 * 1024 rows use it).
+constexpr int kLogitsRows = 1024;
 
 // Timestamp of event ev for this workgroup (thread 0), when tracing is on.
 #define MDX_TRACE(ev)                                                                      \
@@ -446,6 +454,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     __shared__ float att_m[4][2];
     __shared__ float att_l[4][2];
     __shared__ unsigned long long bkey[4];
+    __shared__ float lgs[kLogitsRows];   // this workgroup's logits (host-logits mode)
 
     const int t = threadIdx.x, b = blockIdx.x, lane = t & 63, wave = t >> 6;
     const int L = a.n_layers;
@@ -454,9 +463,15 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         __builtin_amdgcn_make_buffer_rsrc(xb, (short)0, W_TOTAL * 4, 0x00020000);
 
     const unsigned E = __hip_atomic_load(xb + W_CTRL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int pos = a.st->pos;
-    const int mode = a.st->mode;
-    int tok = a.st->token;
+    const int pos = a.in_args ? a.in_pos : a.st->pos;
+    const int mode = a.in_args ? a.in_mode : a.st->mode;
+    int tok = a.in_args ? a.in_token : a.st->token;
+    // a timed-out wait: the device state's flag, and the host's when it reads
+    // the result words without a copy
+    auto flag_timeout = [&]() {
+        __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.res_host) __hip_atomic_store(&a.res_host[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    };
     bool dead = false;
     const unsigned spin_lim = a.spin_limit;
     const bool kv_nt = a.kv_stream != 0;
@@ -1039,7 +1054,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int r = base + lane / PER;
             if ((lane % PER) == 0 && r < re) {
                 const float y = tot * sc;
-                a.logits[r] = y;
+                if (a.logits_host) lgs[r - rb] = y;
+                else a.logits[r] = y;
                 const unsigned long long k = ref_argmax_key(y, r);
                 best = k > best ? k : best;
             }
@@ -1077,9 +1093,15 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * L + 1);
         if (a.trace && t == 0)
             a.trace[(size_t)b * a.trace_stride + 16 * L + 3] = __builtin_amdgcn_s_getreg((3 << 11) | 20);
+        // the logits go to the mapped host buffer as whole rows of 256 values
+        // per store instruction, after the loads (so no poll waits behind
+        // them); workgroup 0 writes its rows after the argmax
+        auto logits_out = [&]() {
+            for (int i = t; i < re - rb; i += NT) a.logits_host[rb + i] = lgs[i];
+        };
         if (b != 0) {
-            if (dead && t == 0)
-                __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.logits_host) logits_out();
+            if (dead && t == 0) flag_timeout();
             return;
         }
         __syncthreads();   // bkey is reused below
@@ -1115,12 +1137,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 st->n_out = st->n_out + 1;
             }
             st->pos = pos + a.advance;
-            if (dead) __hip_atomic_store(&st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (dead) flag_timeout();
+            if (a.res_host) __hip_atomic_store(&a.res_host[0], res, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __hip_atomic_store(xb + W_CTRL, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        if (a.logits_host) logits_out();
         MDX_TRACE(16 * L + 2);
     } else {
-        if (dead && t == 0) __hip_atomic_store(&a.st->pad[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (dead && t == 0) flag_timeout();
         if (b == 0 && t == 0) {
             a.st->pos = pos + a.advance;
             __hip_atomic_store(xb + W_CTRL, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1232,7 +1256,15 @@ int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
     a.trace_stride = p->trace_stride;
     a.spin_limit = p->spin_limit ? p->spin_limit : kSpinLimit;
     a.kv_stream = p->kv_stream;
+    a.in_args = p->in_args;
+    a.in_pos = p->in_pos;
+    a.in_token = p->in_token;
+    a.in_mode = p->in_mode;
+    a.logits_host = p->logits_host;
+    a.res_host = p->res_host;
     if (a.trace && a.trace_stride < 16 * a.n_layers + 4) return -1;
+    // host logits: each workgroup's rows are staged in LDS first
+    if (a.logits_host && (!a.head || (long long)a.vocab > (long long)NB * kLogitsRows)) return -1;
     // MDX_COOP=1 / MDX_COOP=0 force the launch kind over the caller's choice
     // (MDX_COOP=0 serves tools that do not follow cooperative launches).  The
     // grid fits the device one workgroup per CU and every wait is bounded, so a
