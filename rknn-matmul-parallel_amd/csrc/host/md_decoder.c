@@ -1122,12 +1122,14 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
     }
     const int prof = c->profile && c->persist && c->d_trace;
     const int one_launch_head = c->persist && c->persist_head && want_head;
-    /* A plain step with the head in the one launch is host-fed: the position,
-     * token and mode go in as kernel arguments, and the kernel writes the
-     * argmax, the timeout flag and the logits to mapped host memory, so no
-     * copy runs before or after it.  Sampling and profiling steps, which read
-     * the device logits or the trace, keep the copies. */
-    const int host_fed = one_launch_head && !sr && !prof && (long long)c->V <= 256LL * 1024;
+    /* A step with the head in the one launch is host-fed: the position, token
+     * and mode go in as kernel arguments, and the kernel writes the argmax,
+     * the timeout flag and (for a plain step) the logits to mapped host
+     * memory, so no copy runs before or after it.  A sampling step keeps its
+     * logits on the device for the sampler (and copies them out when asked);
+     * a profiling step keeps every copy. */
+    const int host_fed = one_launch_head && !prof && (long long)c->V <= 256LL * 1024;
+    const int host_logits = host_fed && !sr && output_logits;
     if (c->persist) pthread_mutex_lock(&g_persist_mu);
     if (host_fed) {
         c->h_res[0] = -1;
@@ -1137,7 +1139,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
         c->pargs.in_token = embedding ? 0 : token_id;
         c->pargs.in_mode = embedding ? 1 : 0;
         c->pargs.res_host = c->h_res;
-        c->pargs.logits_host = output_logits ? c->h_io : NULL;
+        c->pargs.logits_host = host_logits ? c->h_io : NULL;
         rc = 0;
         if (embedding) {
             memcpy(c->h_io, embedding, (size_t)c->d * 4);
@@ -1163,7 +1165,7 @@ static int do_step(MatmulDecoderContext* c, int token_id, const float* embedding
         if (!rc) rc = launch_seq(c, want_head ? c->g_head : c->g_adv, want_head ? seq_head : seq_adv);
     }
     if (!rc) rc = mdxrt_event_record(c->ev2, c->stream);
-    if (!rc && output_logits && !host_fed)
+    if (!rc && output_logits && !host_logits)
         rc = mdxrt_d2h_async(c->h_io, c->d_logits, (size_t)c->V * 4, c->stream);
     if (!rc && sr) {
         /* penalty and draw on the logits just copied out; the kernels read
