@@ -47,6 +47,10 @@ const char* mdxrt_last_error(void);
 int mdxrt_malloc(void** p, size_t bytes);
 int mdxrt_free(void* p);
 int mdxrt_host_alloc(void** p, size_t bytes);     /* pinned */
+/* Uncached device memory from a process-lifetime pool (never freed: a
+ * released buffer goes back to the pool), zeroed on acquisition. */
+int mdxrt_uc_acquire(void** p, size_t bytes);
+int mdxrt_uc_release(void* p);
 int mdxrt_host_free(void* p);
 int mdxrt_h2d(void* dst, const void* src, size_t bytes);
 int mdxrt_d2h(void* dst, const void* src, size_t bytes);
