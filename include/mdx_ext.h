@@ -60,6 +60,12 @@ int mdx_debug_persist_kv_stream(MatmulDecoderContext* ctx, int mode);
  * timed-out launch that started late could have written); the retry must
  * clear them and still produce the undisturbed result. */
 int mdx_debug_persist_poison_retry(MatmulDecoderContext* ctx);
+/* Test hook (process-wide): on != 0 makes the batch-prefill projections use
+ * the GEMM that loads its activation fragments per wave in rounds instead of
+ * the one that stages the block's activation panel in LDS (same sums, bit for
+ * bit); takes effect for graphs captured afterwards.  Returns the previous
+ * setting. */
+int mdx_debug_gemm_rounds(int on);
 
 /* One decode step of the one-launch path with per-workgroup timestamps
  * (100 MHz device clock) at every stage boundary: out[256][E] with E

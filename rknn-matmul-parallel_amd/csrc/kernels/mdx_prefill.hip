@@ -3,8 +3,9 @@
 // Projections (reference: src/matmul_decoder.c:1841-1899, run_batch_matmul)
 // run on MFMA v_mfma_f32_16x16x32_f16: the qkv and gate/up projections one
 // block per 64 x 32 output tile with the K range split over its waves
-// (k_gemm), the o and down projections split over blocks along K with the
-// activation panel staged in LDS (k_gemm_s).
+// (k_gemm, or k_gemm_p with the block's activation panel staged in LDS), the
+// o and down projections split over blocks along K with the activation panel
+// staged in LDS (k_gemm_s).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -175,6 +176,58 @@ __device__ __forceinline__ void gemm_compute(const GemmRound<KIND>& R, int kb, i
     }
 }
 
+// The epilogue shared by k_gemm and k_gemm_p: the waves' partial tiles (the
+// MFMA accumulators) are summed in LDS in wave order; then split partials go
+// to part (write-through), or the scale and the epilogue are applied.
+template <int NW>
+__device__ __forceinline__ void gemm_epilogue(const float4_t (&acc)[2][4], float (*red)[kMaxM * kNT], int tid,
+                                              int M, int N, int tile, int swiglu, int epi, float sc_a,
+                                              float sc_b, float* out_f32, uint16_t* out_f16, float* part) {
+    const int wave = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    // D fragment: lane holds column c16 of MFMA tile t, rows 16r + 4g + i
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                red[wave][(16 * r + 4 * g + i) * kNT + 16 * t + c16] = acc[t][r][i];
+    __syncthreads();
+    // 2048 outputs over 256 threads, summed in wave order
+    for (int o = tid; o < kMaxM * kNT; o += NW * 64) {
+        const int row = o / kNT, col = o % kNT;
+        if (row >= M) continue;
+        float v = red[0][o];
+#pragma unroll
+        for (int wv = 1; wv < NW; wv++) v = v + red[wv][o];
+        if (part) {
+            const int n = tile * kNT + col;
+            if (n < N) store_wt(&part[((size_t)blockIdx.y * kMaxM + row) * N + n], v);
+            continue;
+        }
+        if (swiglu) {
+            if (col >= kNT / 2) continue;
+            const int cols = N / 2;
+            const int f = tile * (kNT / 2) + col;
+            if (f >= cols) continue;
+            float u = red[0][row * kNT + col + kNT / 2];
+#pragma unroll
+            for (int wv = 1; wv < NW; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
+            const float gs = v * sc_a, us = u * sc_b;
+            float act;
+            if (f < (cols & ~3)) act = silu_mul(gs, us);
+            else act = (gs / (1.0f + expf(-gs))) * us;     // reference tail formula
+            out_f16[(size_t)row * cols + f] = f32_to_f16_bits(act);
+        } else {
+            const int n = tile * kNT + col;
+            if (n >= N) continue;
+            const float y = v * sc_a;
+            float* dst = out_f32 + (size_t)row * N + n;
+            store_wt(dst, epi == 1 ? *dst + y : y);
+        }
+    }
+}
+
 // With part != NULL each block covers K split blockIdx.y (of gridDim.y,
 // possibly 1) and stores its raw partial tile to part[blockIdx.y][row][N]
 // for k_residual_norm; with part == NULL gridDim.y is 1 and the epilogue
@@ -251,48 +304,129 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm(const uint1
         }
     }
 
-    // D fragment: lane holds column c16 of MFMA tile t, rows 16r + 4g + i
+    gemm_epilogue<NW>(acc, red, tid, M, N, tile, swiglu, epi, sc_a, sc_b, out_f32, out_f16, part);
+}
+
+// ---- k_gemm_p: k_gemm with the activation panel staged in LDS -------------
+//
+// The same tiles, K partition and reduction as k_gemm (so the same sums, bit
+// for bit), but the block first requests all of its waves' weights, then
+// stages the 64-row activation panel of its K split (at most kPanelK wide)
+// in LDS with every load issued at once, and the waves read their MFMA A
+// fragments from there.  k_gemm loads those fragments per wave in dependent
+// rounds, so each wave of a block fetches its own share of the panel as it
+// goes; here one round trip brings the whole panel and the weights.  The
+// reduction buffer reuses the panel's LDS (gfx950: 160 KB per CU).
+constexpr int kPanelK = 1024;
+constexpr int kPanelRS = kPanelK / 8 + 1;   // uint4 per LDS panel row (16-byte pad)
+
+template <int KIND>
+__global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm_p(const uint16_t* __restrict__ x16,
+                                                            int M, const uint8_t* __restrict__ w, int K,
+                                                            int N, const float* scale, int epi,
+                                                            float* out_f32, uint16_t* out_f16, float* part) {
+    using GK = GemmKind<KIND>;
+    constexpr int EPL = GK::EPL, KB = 4 * EPL, STEPS = EPL / 8;
+    constexpr int NW = GK::WAVES;
+    constexpr int KPW = (kPanelK / KB + NW - 1) / NW;   // K-blocks per wave at most
+    static_assert(kMaxM * kPanelRS * 16 >= NW * kMaxM * kNT * 4, "the reduction fits the panel");
+    __shared__ uint4 xs4[kMaxM * kPanelRS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tile = blockIdx.x;
+    const int swiglu = epi == 2;
+    const int g = lane >> 4, c16 = lane & 15;
+    const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
+    const int nkb_all = K / KB;
+    const int per_split = (nkb_all + gridDim.y - 1) / gridDim.y;
+    const int sb0 = min(nkb_all, (int)blockIdx.y * per_split);
+    const int sb1 = min(nkb_all, sb0 + per_split);
+    const int per = (sb1 - sb0 + NW - 1) / NW;
+    const int kb0 = min(sb1, sb0 + wave * per), kb1 = min(sb1, kb0 + per);
+
+    // this wave's weights: K-blocks kb0 .. kb1-1 of the tile's two 16-row groups
+    uint4 bw[KPW][2];
+    {
+        bool wvalid[2];
+        const uint8_t* wrow[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int r = tile_row(tile, 16 * t + c16, swiglu, N);
+            wvalid[t] = r < N;
+            wrow[t] = w + (size_t)(wvalid[t] ? r : 0) * row_bytes;
+        }
+#pragma unroll
+        for (int j = 0; j < KPW; j++) {
+            const int kb = min(kb0 + j, kb1 - 1);
+            const int k = (kb < kb0 ? kb0 : kb) * KB + g * EPL;
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+                bw[j][t] = (wvalid[t] && kb0 + j < kb1) ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
+                                                       : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    float sc_a = 1.0f, sc_b = 1.0f;
+    if (!part && scale) {
+        const int col = tid % kNT;
+        if (swiglu) {
+            const int f = tile * (kNT / 2) + col;
+            if (col < kNT / 2 && f < N / 2) {
+                sc_a = scale[f];
+                sc_b = scale[N / 2 + f];
+            }
+        } else if (tile * kNT + col < N) {
+            sc_a = scale[tile * kNT + col];
+        }
+    }
+    // the panel: 64 rows (rows >= M repeat row M-1) x this split's K range
+    const int ks0 = sb0 * KB, kw = (sb1 - sb0) * KB;
+    {
+        constexpr int PER = kMaxM * (kPanelK / 8) / (NW * 64);
+        static_assert(kMaxM * (kPanelK / 8) % (NW * 64) == 0, "panel split");
+        const int cpr = kw / 8;                  // uint4 per panel row
+        uint4 v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = tid + i * NW * 64;
+            const int row = c / cpr, col = c % cpr;
+            const int rr = row < M ? row : M - 1;
+            v[i] = row < kMaxM ? *reinterpret_cast<const uint4*>(x16 + (size_t)rr * K + ks0 + 8 * col)
+                               : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int c = tid + i * NW * 64;
+            const int row = c / cpr, col = c % cpr;
+            if (row < kMaxM) xs4[row * kPanelRS + col] = v[i];
+        }
+    }
+    __syncthreads();
+
+    float4_t acc[2][4];
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < 4; r++) acc[t][r] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                red[wave][(16 * r + 4 * g + i) * kNT + 16 * t + c16] = acc[t][r][i];
-    __syncthreads();
-    // 2048 outputs over 256 threads, summed in wave order
-    for (int o = tid; o < kMaxM * kNT; o += NW * 64) {
-        const int row = o / kNT, col = o % kNT;
-        if (row >= M) continue;
-        float v = red[0][o];
+    for (int j = 0; j < KPW; j++) {
+        if (kb0 + j >= kb1) break;
+        const int kl = (kb0 + j - sb0) * KB + g * EPL;   // k within the panel
+        half8_t b[2][STEPS];
 #pragma unroll
-        for (int wv = 1; wv < NW; wv++) v = v + red[wv][o];
-        if (part) {
-            const int n = tile * kNT + col;
-            if (n < N) store_wt(&part[((size_t)blockIdx.y * kMaxM + row) * N + n], v);
-            continue;
-        }
-        if (swiglu) {
-            if (col >= kNT / 2) continue;
-            const int cols = N / 2;
-            const int f = tile * (kNT / 2) + col;
-            if (f >= cols) continue;
-            float u = red[0][row * kNT + col + kNT / 2];
+        for (int t = 0; t < 2; t++) widen_b<KIND>(bw[j][t], b[t]);
 #pragma unroll
-            for (int wv = 1; wv < NW; wv++) u = u + red[wv][row * kNT + col + kNT / 2];
-            const float gs = v * sc_a, us = u * sc_b;
-            float act;
-            if (f < (cols & ~3)) act = silu_mul(gs, us);
-            else act = (gs / (1.0f + expf(-gs))) * us;     // reference tail formula
-            out_f16[(size_t)row * cols + f] = f32_to_f16_bits(act);
-        } else {
-            const int n = tile * kNT + col;
-            if (n >= N) continue;
-            const float y = v * sc_a;
-            float* dst = out_f32 + (size_t)row * N + n;
-            store_wt(dst, epi == 1 ? *dst + y : y);
-        }
+        for (int s = 0; s < STEPS; s++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const half8_t a = __builtin_bit_cast(half8_t, xs4[(16 * r + c16) * kPanelRS + kl / 8 + s]);
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+                    acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[t][s], acc[t][r], 0, 0, 0);
+            }
     }
+    __syncthreads();   // the panel's LDS is reused for the reduction
+    gemm_epilogue<NW>(acc, reinterpret_cast<float (*)[kMaxM * kNT]>(xs4), tid, M, N, tile, swiglu, epi, sc_a,
+                      sc_b, out_f32, out_f16, part);
 }
 
 // ---- projections, split-K over blocks: k_gemm_s -------------------------------
@@ -770,6 +904,11 @@ size_t mdx_gemm_scratch_floats(int M, int N, int K) {
 
 
 
+// Test hook: 1 selects k_gemm (fragments loaded in rounds) where k_gemm_p
+// would serve.  Not thread-safe: set it before the contexts it is meant for
+// capture their prefill graphs.
+static int g_gemm_rounds = 0;
+
 static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
                        float* part, int ns, void* stream) {
     const int kb = w->kind == MDX_W_F16 ? 32 : (w->kind == MDX_W_I8 ? 64 : 128);
@@ -784,6 +923,32 @@ static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilo
     const uint8_t* wp = (const uint8_t*)w->w;
     float* of = (float*)out;
     uint16_t* oh = (uint16_t*)out;
+    // The panel kernel when every split's K range fits the LDS panel: for the
+    // SwiGLU GEMM (M=60, one split of 1024: fp16 11.80 -> 10.58 us per launch,
+    // int8 9.23 -> 8.96, int4 9.03 -> 8.46) and, with fp16 weights, for split
+    // partials (qkv, two splits of 512: 7.42 -> 7.33 us; int8 and int4 6.03 ->
+    // 6.39 and 6.01 -> 6.20, so those keep k_gemm).
+    const int nkb = w->K / kb, per_split = (nkb + ns - 1) / ns;
+    const bool panel = per_split * kb <= kPanelK && (epilogue == 2 || w->kind == MDX_W_F16);
+    if (panel && !g_gemm_rounds) {
+        switch (w->kind) {
+            case MDX_W_F16:
+                hipLaunchKernelGGL(k_gemm_p<MDX_W_F16>, grid, block, 0, (hipStream_t)stream, x16, M, wp,
+                                   w->K, w->N, w->scale, epilogue, of, oh, part);
+                break;
+            case MDX_W_I8:
+                hipLaunchKernelGGL(k_gemm_p<MDX_W_I8>, grid, block, 0, (hipStream_t)stream, x16, M, wp,
+                                   w->K, w->N, w->scale, epilogue, of, oh, part);
+                break;
+            case MDX_W_I4:
+                hipLaunchKernelGGL(k_gemm_p<MDX_W_I4>, grid, block, 0, (hipStream_t)stream, x16, M, wp,
+                                   w->K, w->N, w->scale, epilogue, of, oh, part);
+                break;
+            default:
+                return -5;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     switch (w->kind) {
         case MDX_W_F16:
             hipLaunchKernelGGL(k_gemm<MDX_W_F16>, grid, block, 0, (hipStream_t)stream, x16, M, wp, w->K,
@@ -801,6 +966,12 @@ static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilo
             return -5;
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int mdx_debug_gemm_rounds(int on) {
+    const int old = g_gemm_rounds;
+    g_gemm_rounds = on != 0;
+    return old;
 }
 
 int mdx_launch_gemm(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,

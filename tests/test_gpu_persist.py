@@ -286,6 +286,34 @@ def test_prefill_full_width_matches_oracle(mdx, gpu, oracle_lib, models, quant, 
     assert g.seq_len == o.seq_len == 2 * M
 
 
+@pytest.mark.parametrize("quant", [0, 1, 2])
+def test_prefill_panel_gemm_is_bit_identical(mdx, gpu, oracle_lib, models, quant):
+    """The batch-prefill projections with the activation panel staged in LDS
+    (k_gemm_p, the default where a K split fits 1024) against the GEMM that
+    loads its fragments per wave in rounds (k_gemm, selected by the test
+    hook): the same K partition and summation order, so the logits and every
+    K/V row are the same bits, over M = 60, 17 and 1 on top of each other."""
+    cfg, get = models
+    rng = np.random.default_rng(900 + quant)
+    embs = [rng.standard_normal((m, 1024)).astype(np.float32) for m in (60, 17, 1)]
+    runs = []
+    for rounds in (0, 1):
+        prev = mdx.lib().mdx_debug_gemm_rounds(rounds)
+        try:
+            g, _ = _pair(mdx, oracle_lib, cfg, get(quant), quant)
+            out = [g.prefill_logits(e) for e in embs]
+            kv = [g.kv_read(layer, 0, 78) for layer in (0, 1)]
+            g.close()
+        finally:
+            mdx.lib().mdx_debug_gemm_rounds(prev)
+        runs.append((out, kv))
+    (oa, ka), (ob, kb) = runs
+    for (ta, la), (tb, lb) in zip(oa, ob):
+        assert ta == tb and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    for (k1, v1), (k2, v2) in zip(ka, kb):
+        assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
 def test_timed_out_launch_is_retried_cooperatively(mdx, gpu, oracle_lib, models, capfd):
     """A one-launch step whose waits give up (forced here with a 1-round spin
     limit, as a grid that is not co-resident would) reports the timeout in the
