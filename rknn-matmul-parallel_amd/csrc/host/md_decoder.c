@@ -712,8 +712,19 @@ static void setup_persist(MatmulDecoderContext* c) {
     /* The exchange words in uncached memory: the stores and polls then skip
      * the L2 (fp16 layers at KV 512: 465.3 -> 443.8 us/token).  The arena's
      * words stay the fallback if that allocation fails. */
-    if (mdxrt_uc_acquire(&c->uc_xbuf, mdx_persist_xbuf_bytes()) == 0) c->d_xbuf = c->uc_xbuf;
-    else c->uc_xbuf = NULL;
+    if (mdxrt_uc_acquire(&c->uc_xbuf, mdx_persist_xbuf_bytes()) == 0) {
+        /* a pooled buffer holds the words of an earlier context: start from
+         * zero words (epoch 0 is never valid) */
+        if (mdxrt_fill_u32(c->uc_xbuf, 0u, mdx_persist_xbuf_bytes() / 4, c->stream) ||
+            mdxrt_stream_sync(c->stream)) {
+            mdxrt_uc_release(c->uc_xbuf);
+            c->uc_xbuf = NULL;
+        } else {
+            c->d_xbuf = c->uc_xbuf;
+        }
+    } else {
+        c->uc_xbuf = NULL;
+    }
     a->xbuf = c->d_xbuf;
     c->persist = 1;
 }

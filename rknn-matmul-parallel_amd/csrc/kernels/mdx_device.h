@@ -48,7 +48,8 @@ int mdxrt_malloc(void** p, size_t bytes);
 int mdxrt_free(void* p);
 int mdxrt_host_alloc(void** p, size_t bytes);     /* pinned */
 /* Uncached device memory from a process-lifetime pool (never freed: a
- * released buffer goes back to the pool), zeroed on acquisition. */
+ * released buffer goes back to the pool).  Not cleared: the caller clears it
+ * on its stream. */
 int mdxrt_uc_acquire(void** p, size_t bytes);
 int mdxrt_uc_release(void* p);
 int mdxrt_host_free(void* p);

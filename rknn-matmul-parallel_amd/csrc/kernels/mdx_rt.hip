@@ -41,7 +41,9 @@ __global__ void k_fill_u32(uint32_t* dst, uint32_t value, size_t n) {
 // has read is never returned to the device before the process ends (later
 // allocations at the same addresses have held wrong values), so released
 // buffers go back to this pool, one list per device, and are handed out
-// again to later contexts.
+// again to later contexts.  The caller clears a buffer it acquires (on its
+// own stream: nothing here synchronises the device, which could meet another
+// thread's graph capture).
 namespace {
 struct UcBuf {
     int dev;
@@ -74,7 +76,6 @@ int mdxrt_free(void* p) {
     return 0;
 }
 
-
 int mdxrt_uc_acquire(void** p, size_t bytes) {
     *p = nullptr;
     int dev = 0;
@@ -94,9 +95,6 @@ int mdxrt_uc_acquire(void** p, size_t bytes) {
         g_uc->push_back(UcBuf{dev, bytes, q, true});
         *p = q;
     }
-    // a new context starts from zero words (epoch 0 is never valid)
-    MDX_CHECK(hipMemset(*p, 0, bytes), "hipMemset");
-    MDX_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
     return 0;
 }
 
