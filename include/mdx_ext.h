@@ -55,6 +55,14 @@ int mdx_debug_persist_spin_limit(MatmulDecoderContext* ctx, unsigned rounds);
  * context does not evict the lm_head from the last-level cache; 0 / 1: always
  * ordinary / always non-temporal.  The results are the same either way. */
 int mdx_debug_persist_kv_stream(MatmulDecoderContext* ctx, int mode);
+/* Test hook: where the one-launch step's per-head exchanges (qkv rows to
+ * attention, partial records to the merge) travel.  -1 (the default): in the
+ * L2 of the XCD that the KV head's workgroups share, through a cacheable word
+ * buffer, until a step times out, then through the uncached words like the
+ * other exchanges; 0 / 1: always through the uncached words / always local.
+ * The results are the same bits either way.  Returns
+ * MATMUL_DECODER_ERR_UNSUPPORTED when the context has no local buffer. */
+int mdx_debug_persist_local_exchange(MatmulDecoderContext* ctx, int mode);
 /* Test hook: before the next cooperative retry, leave exchange words tagged
  * with the epoch that retry would accept first (what a workgroup of the
  * timed-out launch that started late could have written); the retry must

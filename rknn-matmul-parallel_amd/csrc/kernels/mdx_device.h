@@ -192,6 +192,10 @@ typedef struct {
                                           of logits */
     int* res_host;                     /* optional mapped host words: [0] <- the argmax,
                                           [1] <- 1 when a wait timed out */
+    void* xbl;                         /* optional: cacheable words (mdx_persist_xbuf_bytes(),
+                                          zeroed) for the exchanges among one KV head's
+                                          workgroups, which share an XCD; NULL: those go
+                                          through xbuf like the others */
 } mdx_persist_args;
 
 /* 1 when (d, nq, nkv, hd, F) is the shape the persistent step is built for. */

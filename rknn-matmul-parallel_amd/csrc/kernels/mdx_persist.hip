@@ -103,6 +103,7 @@ struct PArgs {
     int in_pos, in_token, in_mode;
     float* logits_host;         // optional mapped host buffer for the logits (instead of logits)
     int* res_host;              // optional mapped host words: [0] the argmax, [1] set on a timeout
+    unsigned* xbl;              // optional cacheable words for the per-head exchanges
 };
 
 // Rows of the lm_head per workgroup that the host-logits mode stages in LDS
@@ -120,8 +121,9 @@ constexpr int kLogitsRows = 1024;
 // Cache policy sc1: bypass the non-coherent caches.  The buffer-load builtin
 // is a plain read to the optimiser, so the polling loop below carries a
 // compiler memory barrier to keep the reload inside the loop.
+template <int AUX = 16>
 __device__ __forceinline__ u32x4 ll_load(__amdgpu_buffer_rsrc_t rs, int word) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, 16);
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, word * 4, 0, AUX);
 }
 __device__ __forceinline__ bool ll_ok(u32x4 v, unsigned ep) {
     return ((v.x >> 16) == ep) & ((v.y >> 16) == ep) & ((v.z >> 16) == ep) & ((v.w >> 16) == ep);
@@ -138,6 +140,17 @@ __device__ __forceinline__ void ll_put(unsigned* xb, int word, unsigned payload,
 // so a reader never accepts a partly written group).
 __device__ __forceinline__ void ll_put4(__amdgpu_buffer_rsrc_t rs, int word, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, rs, word * 4, 0, 16);
+}
+
+// The per-head exchanges (qkv rows -> attention, partial records -> merge)
+// have their writers and readers among the 32 workgroups of one KV head, and
+// workgroups b, b + 8, ... run on one XCD: with a cacheable word buffer those
+// exchanges can stay in that XCD's L2.  Plain stores (through to the L2) and
+// non-temporal polls (which do not hit a stale line in the CU's L1; polls with
+// sc0, or an L1 invalidate before each poll, kept reading stale words).
+constexpr int kLocalPoll = 2;   // nt
+__device__ __forceinline__ void lx_put4(__amdgpu_buffer_rsrc_t rs, int word, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rs, word * 4, 0, 0);
 }
 __device__ __forceinline__ u32x4 ll_pack2(float v0, float v1, unsigned ep) {
     const unsigned x = __float_as_uint(v0), y = __float_as_uint(v1), e = ep << 16;
@@ -166,11 +179,11 @@ __device__ __forceinline__ void put_hidden4(__amdgpu_buffer_rsrc_t rs, int base,
 
 // Polls N 16-byte groups until every word carries epoch ep.  Returns false
 // after `limit` rounds (the data is then stale; the caller stops waiting).
-template <int N>
+template <int N, int AUX = 16>
 __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&word)[N],
                                         u32x4 (&v)[N], unsigned ep, bool dead, unsigned limit) {
 #pragma unroll
-    for (int i = 0; i < N; i++) v[i] = ll_load(rs, word[i]);
+    for (int i = 0; i < N; i++) v[i] = ll_load<AUX>(rs, word[i]);
     if (dead) return true;
     for (unsigned spin = 0;; spin++) {
         asm volatile("" ::: "memory");
@@ -179,7 +192,7 @@ __device__ __forceinline__ bool ll_wait(__amdgpu_buffer_rsrc_t rs, const int (&w
         for (int i = 0; i < N; i++) {
             if (!ll_ok(v[i], ep)) {
                 all = false;
-                v[i] = ll_load(rs, word[i]);
+                v[i] = ll_load<AUX>(rs, word[i]);
             }
         }
         if (all) return true;
@@ -461,6 +474,10 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
     unsigned* xb = a.xbuf;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(xb, (short)0, W_TOTAL * 4, 0x00020000);
+    // per-head exchanges: in the XCD's L2 when a cacheable buffer is given
+    const bool lx = a.xbl != nullptr;
+    const __amdgpu_buffer_rsrc_t rsl =
+        __builtin_amdgcn_make_buffer_rsrc(lx ? a.xbl : xb, (short)0, W_TOTAL * 4, 0x00020000);
 
     const unsigned E = __hip_atomic_load(xb + W_CTRL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int pos = a.in_args ? a.in_pos : a.st->pos;
@@ -620,8 +637,11 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 y = y * sclA;
             }
             const float y1 = __shfl_down(y, 1, 64);
-            if (t < 16 && (t & 1) == 0)
-                ll_put4(rs, W_QKV + j * 1024 + 2 * (s * 16 + t), ll_pack2(y, y1, ep));
+            if (t < 16 && (t & 1) == 0) {
+                const int w = W_QKV + j * 1024 + 2 * (s * 16 + t);
+                if (lx) lx_put4(rsl, w, ll_pack2(y, y1, ep));
+                else ll_put4(rs, w, ll_pack2(y, y1, ep));
+            }
         }
         MDX_TRACE(16 * l + 2);
 
@@ -634,7 +654,8 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const bool need = t < 128 || has_new;
             int wd[1] = {W_QKV + j * 1024 + 4 * t};
             u32x4 v[1];
-            const bool ok = ll_wait<1>(rs, wd, v, ep, dead || !need, spin_lim);
+            const bool ok = lx ? ll_wait<1, kLocalPoll>(rsl, wd, v, ep, dead || !need, spin_lim)
+                               : ll_wait<1>(rs, wd, v, ep, dead || !need, spin_lim);
             qkv_s[2 * t] = ll_f32(v[0].x, v[0].y);
             qkv_s[2 * t + 1] = ll_f32(v[0].z, v[0].w);
             if (__syncthreads_or(!ok)) dead = true;
@@ -803,10 +824,15 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             if (t < 128) {
                 // values v, v + 1 of head v >> 7: dimension block dd >> 3, slot dd & 7
                 const int v = 2 * t, h2 = v >> 7, dd = v & 127;
-                ll_put4(rs, jb + ((h2 * 16 + (dd >> 3)) * GRP + s) * 16 + 2 * (dd & 7),
-                        ll_pack2(po[v], po[v + 1], ep));
+                const int w = jb + ((h2 * 16 + (dd >> 3)) * GRP + s) * 16 + 2 * (dd & 7);
+                if (lx) lx_put4(rsl, w, ll_pack2(po[v], po[v + 1], ep));
+                else ll_put4(rs, w, ll_pack2(po[v], po[v + 1], ep));
             }
-            if (d == 0) ll_put4(rs, jb + PART_O + (hh * GRP + s) * 4, ll_pack2(runM, runL, ep));
+            if (d == 0) {
+                const int w = jb + PART_O + (hh * GRP + s) * 4;
+                if (lx) lx_put4(rsl, w, ll_pack2(runM, runL, ep));
+                else ll_put4(rs, w, ll_pack2(runM, runL, ep));
+            }
         }
         MDX_TRACE(16 * l + 4);
 
@@ -822,7 +848,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             const int ob = jb + (hh * 16 + c) * GRP * 16;
             int wd[3] = {jb + PART_O + (hh * GRP + (lane & 31)) * 4, ob + 4 * lane, ob + 256 + 4 * lane};
             u32x4 v[3];
-            if (!ll_wait<3>(rs, wd, v, ep, dead, spin_lim)) dead = true;
+            if (!(lx ? ll_wait<3, kLocalPoll>(rsl, wd, v, ep, dead, spin_lim)
+                     : ll_wait<3>(rs, wd, v, ep, dead, spin_lim)))
+                dead = true;
             const float m = ll_f32(v[0].x, v[0].y);
             const float M = half_max_dpp(m);
             const float w = m == -INFINITY ? 0.0f : exp2_fast(m - M);
@@ -1262,6 +1290,7 @@ int mdx_launch_persist_step(const mdx_persist_args* p, void* stream) {
     a.in_mode = p->in_mode;
     a.logits_host = p->logits_host;
     a.res_host = p->res_host;
+    a.xbl = reinterpret_cast<unsigned*>(p->xbl);
     if (a.trace && a.trace_stride < 16 * a.n_layers + 4) return -1;
     // host logits: each workgroup's rows are staged in LDS first
     if (a.logits_host && (!a.head || (long long)a.vocab > (long long)NB * kLogitsRows)) return -1;

@@ -127,6 +127,7 @@ def lib() -> C.CDLL:
             "mdx_decode_path": (C.c_int, [P]),
             "mdx_debug_persist_spin_limit": (C.c_int, [P, C.c_uint]),
             "mdx_debug_persist_kv_stream": (C.c_int, [P, C.c_int]),
+            "mdx_debug_persist_local_exchange": (C.c_int, [P, C.c_int]),
             "mdx_debug_persist_poison_retry": (C.c_int, [P]),
             "mdx_trace_step": (C.c_int, [P, C.c_int, C.POINTER(C.c_uint64), C.c_int]),
             "mdx_kv_fill_normal": (C.c_int, [P, C.c_int, C.c_uint64]),
@@ -390,6 +391,10 @@ class Decoder:
     def force_kv_stream(self, mode: int):
         """K/V load policy of the one-launch step: -1 auto, 0 ordinary, 1 non-temporal."""
         _check(lib().mdx_debug_persist_kv_stream(self.h, mode), "kv_stream")
+
+    def force_local_exchange(self, mode: int):
+        """Per-head exchanges of the one-launch step: -1 auto, 0 through memory, 1 in the L2."""
+        _check(lib().mdx_debug_persist_local_exchange(self.h, mode), "local_exchange")
 
     def close(self):
         if self.h:

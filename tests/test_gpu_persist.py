@@ -91,6 +91,38 @@ def test_step_matches_oracle(mdx, gpu, oracle_lib, models, quant, n_pos):
     assert g.seq_len == n_pos + 1
 
 
+@pytest.mark.parametrize("quant,n_pos", [(0, 0), (0, 33), (0, 600), (2, 600), (1, 4100), (2, 4100)])
+def test_local_exchange_is_bit_identical(mdx, gpu, oracle_lib, models, quant, n_pos):
+    """The per-head exchanges of the one-launch step (qkv rows to attention,
+    partial records to the merge) through the XCD's L2 (the default) or
+    through the uncached words like the other exchanges: only the transport
+    differs, so three steps give the same logits, tokens and K/V rows, and
+    the local path matches the oracle."""
+    cfg, get = models
+    path = get(quant)
+    runs = []
+    for mode in (1, 0):
+        g, o = _pair(mdx, oracle_lib, cfg, path, quant)
+        g.force_local_exchange(mode)
+        g.kv_fill_normal(n_pos, 61)
+        out = []
+        tok = 777
+        for _ in range(3):
+            tok, lg = g.step(tok)
+            out.append((tok, lg.copy()))
+        k, v = g.kv_read(1, n_pos, 3)
+        runs.append((out, k.copy(), v.copy()))
+        if mode == 1:
+            assert o.kv_fill_normal(n_pos, 61) == 0
+            to, lo = o.step(777)
+            assert cosine(out[0][1], lo) >= 0.9999 and rel_err(out[0][1], lo) <= 2e-3
+        g.close()
+    (a, ka, va), (b, kb, vb) = runs
+    for (ta, la), (tb, lb) in zip(a, b):
+        assert ta == tb and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
 @pytest.mark.parametrize("n_pos", [33, 600, 4100])
 def test_kv_load_policy_is_bit_identical(mdx, gpu, oracle_lib, models, n_pos):
     """The K/V rows read with ordinary or with non-temporal loads (the policy
