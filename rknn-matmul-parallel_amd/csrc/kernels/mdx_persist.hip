@@ -568,7 +568,13 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         const float* qknw = wave < 2 ? Ly.q_norm : Ly.k_norm;
         const float rn0 = qknw ? qknw[ri0] : 1.0f;
         const float rn1 = qknw ? qknw[ri1] : 1.0f;
-        const float sclA = Ly.sqkv ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
+        // int4 layers: the column scales are requested by wave 0 alone, which
+        // applies them, and the SwiGLU epilogue reads the gate and up sums of
+        // its feature straight from the reduction (W4A16 KV 4000 497.7 -> 486.1
+        // us/token, tokens unchanged; the same code measured +0.7 us with fp16
+        // and +1.8 us with int8 layers at KV 512, so those keep the form below)
+        constexpr bool kLean = KIND == MDX_W_I4;
+        const float sclA = Ly.sqkv && (!kLean || wave == 0) ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
         if (l > 0) {
             const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
@@ -636,7 +642,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 if (SA::NSPLIT == 2) y = y + red[t * SA::NSPLIT + 1];
                 y = y * sclA;
             }
-            const float y1 = __shfl_down(y, 1, 64);
+            const float y1 = kLean ? dpp<0x101>(y) : __shfl_down(y, 1, 64);   // lane t + 1's y
             if (t < 16 && (t & 1) == 0) {
                 const int w = W_QKV + j * 1024 + 2 * (s * 16 + t);
                 if (lx) lx_put4(rsl, w, ll_pack2(y, y1, ep));
@@ -902,7 +908,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * l + 5);
 
         // ================= D: o projection + residual ==========
-        const float sclD = Ly.so ? Ly.so[4 * b + (t & 3)] : 1.0f;
+        const float sclD = Ly.so && (!kLean || wave == 0) ? Ly.so[4 * b + (t & 3)] : 1.0f;
         {
             // waves 1 and 2 gather the attention output: thread u reads the
             // 16-byte groups u + 128 k (4 values each), k < 4
@@ -962,7 +968,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             }
         }
         const float4 nwE = reinterpret_cast<const float4*>(Ly.post_norm)[t];
-        const float sclE = Ly.sgu ? Ly.sgu[rowE(t < 24 ? t : 0)] : 1.0f;
+        const float sclE = Ly.sgu && (!kLean || wave == 0) ? Ly.sgu[rowE(kLean ? (t < 12 ? t : 0) : (t < 24 ? t : 0))]
+                                                           : 1.0f;
+        const float sclU = kLean && Ly.sgu && wave == 0 ? Ly.sgu[rowE(t < 12 ? t + 12 : 12)] : 1.0f;
         {
             const int wb = W_HO + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
@@ -984,14 +992,28 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         rm_dot<KIND, 24, D>(wE, xs4, red, t);
         __syncthreads();
         if (wave == 0) {
-            // lane k < 24: row k (gate k < 12, up k - 12); lane k < 12 then
-            // holds feature k's activation, broadcast with readlane
-            const int r = lane < 24 ? lane : 0;
-            float y = red[r * SE::NSPLIT];
-            if (SE::NSPLIT == 2) y = y + red[r * SE::NSPLIT + 1];
-            y = y * sclE;
-            const float u = __shfl(y, (lane + 12) & 63, 64);
-            const unsigned act = f32_to_f16_bits(silu_mul(y, u));
+            unsigned act;
+            if constexpr (kLean) {
+                // lane k < 12: feature k, the gate row k and the up row k + 12
+                const int r = lane < 12 ? lane : 0;
+                float y = red[r * SE::NSPLIT];
+                float u = red[(r + 12) * SE::NSPLIT];
+                if (SE::NSPLIT == 2) {
+                    y = y + red[r * SE::NSPLIT + 1];
+                    u = u + red[(r + 12) * SE::NSPLIT + 1];
+                }
+                act = f32_to_f16_bits(silu_mul(y * sclE, u * sclU));
+            } else {
+                // lane k < 24: row k (gate k < 12, up k - 12); lane k < 12 then
+                // holds feature k's activation
+                const int r = lane < 24 ? lane : 0;
+                float y = red[r * SE::NSPLIT];
+                if (SE::NSPLIT == 2) y = y + red[r * SE::NSPLIT + 1];
+                y = y * sclE;
+                const float u = __shfl(y, (lane + 12) & 63, 64);
+                act = f32_to_f16_bits(silu_mul(y, u));
+            }
+            // feature k's activation, broadcast with readlane
             unsigned av[12];
 #pragma unroll
             for (int k = 0; k < 12; k++) av[k] = __builtin_amdgcn_readlane(act, k);
@@ -1010,7 +1032,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         MDX_TRACE(16 * l + 9);
 
         // ================= F: down projection + residual ==========
-        const float sclF = Ly.sdown ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
+        const float sclF = Ly.sdown && (!kLean || wave == 0) ? Ly.sdown[4 * b + (t & 3)] : 1.0f;
         MDX_TRACE(16 * l + 15);
         {
             // thread t reads the 16-byte groups t, t + 256, t + 512; group g
