@@ -74,6 +74,20 @@ int mdx_debug_persist_poison_retry(MatmulDecoderContext* ctx);
  * bit); takes effect for graphs captured afterwards.  Returns the previous
  * setting. */
 int mdx_debug_gemm_rounds(int on);
+/* The K-split count of a batch-prefill projection that is split over blocks
+ * (kind MDX_W_F16/I8/I4, N outputs, K inputs), with the K-blocks per split in
+ * *per_split (may be NULL): split s covers K-blocks [s*per, (s+1)*per), and
+ * no split is empty.  Host arithmetic only (no device call); -1 for invalid
+ * arguments. */
+int mdx_debug_gemm_splits(int kind, int N, int K, int* per_split);
+/* Host enumeration of the K/V cache rows the one-launch decode step reads,
+ * with the kernel's own split and row functions: every position
+ * 0 <= pos < max_seq, every attention split, every round of k_passes (4 or
+ * 5) 16-position passes the step requests.  Returns the number of rows
+ * outside [0, pos] (0 when every address lies in the cache rows written so
+ * far), -1 for invalid arguments; *n_checked (may be NULL) receives the
+ * number of row addresses checked.  No device call. */
+long long mdx_debug_persist_kv_rows(int max_seq, int k_passes, long long* n_checked);
 
 /* One decode step of the one-launch path with per-workgroup timestamps
  * (100 MHz device clock) at every stage boundary: out[256][E] with E
@@ -216,7 +230,10 @@ int matmul_decoder_step_sample(MatmulDecoderContext* ctx, int token_id, const fl
  * with a message: the scratch holds 1024 candidates).  Enqueued on `stream`
  * (NULL: the default stream); returns without synchronising.  It calls no
  * allocator: its 141 KB of scratch is a static device array of the library,
- * one per GPU, held until the process ends.  Calls that overlap on one GPU
+ * one per GPU, held until the process ends.  The first call on each device
+ * looks up that array's device address (hipGetSymbolAddress), so make it
+ * outside stream capture; later calls can be captured (they launch kernels
+ * only, no memset nodes).  Calls that overlap on one GPU
  * share that scratch and race; serialise them.  Returns 0, -1 for bad
  * arguments, -4 on a HIP failure. */
 int mdx_sample_topk_noalloc(const float* logits, int V, float temperature, int top_k, float top_p,

@@ -49,6 +49,28 @@ constexpr int QD = NQ * HD, KVD = NKV * HD;
 constexpr int GRP = NB / NKV;           // workgroups per KV head
 constexpr unsigned kSpinLimit = 1u << 18;   // polling rounds before a wait gives up
 
+// Attention split of a step at position pos: split s (of GRP per KV head)
+// covers positions [p0, p0 + n) of the Lk = pos + 1 cached ones.  The cache
+// row a K/V load reads for position index pi of the split: the position
+// itself while pi < n and it is not the step's own (that row is appended by
+// this step and taken from registers), else row 0 as a stand-in for an
+// unused slot, so every address lies in rows [0, pos].  Shared by the kernel
+// and by mdx_debug_persist_kv_rows, which enumerates it on the host.
+struct KvSplit {
+    int p0, n;
+};
+__host__ __device__ inline KvSplit kv_split(int pos, int s) {
+    const int Lk = pos + 1;
+    const int cks = (Lk + GRP - 1) / GRP;
+    const int p0 = s * cks;
+    const int p1 = Lk < p0 + cks ? Lk : p0 + cks;
+    return KvSplit{p0, p1 > p0 ? p1 - p0 : 0};
+}
+__host__ __device__ inline int kv_row(const KvSplit& sp, int pi, int pos) {
+    const int p = sp.p0 + pi;
+    return (pi < sp.n && p != pos) ? p : 0;
+}
+
 // exchange buffer layout, in 32-bit words
 constexpr int W_CTRL = 0;                          // [0] step counter
 constexpr int W_QKV = 16;                          // [NKV][512 values][2]
@@ -495,11 +517,9 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 
     // attention work split of this workgroup
     const int j = b % NKV, s = b / NKV;
-    const int Lk = pos + 1;
-    const int cks = (Lk + GRP - 1) / GRP;
-    const int p0 = s * cks;
-    const int p1 = min(Lk, p0 + cks);
-    const int n = p1 > p0 ? p1 - p0 : 0;
+    const KvSplit ksp = kv_split(pos, s);
+    const int p0 = ksp.p0, n = ksp.n;
+    const int p1 = p0 + n;
     const bool has_new = pos >= p0 && pos < p1;
     const int pl = t >> 4, dl = t & 15;
 
@@ -597,18 +617,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
             if (kv_nt) {
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
-                    const int pi = 16 * (q0 + qq) + pl;
-                    const int p = p0 + pi;
-                    const size_t off = (size_t)((pi < n && p != pos) ? p : 0) * KVD + j * HD + dl * 8;
+                    const size_t off = (size_t)kv_row(ksp, 16 * (q0 + qq) + pl, pos) * KVD + j * HD + dl * 8;
                     kk[qq] = ld_nt(Ly.kc + off);
                     vv[qq] = ld_nt(Ly.vc + off);
                 }
             } else {
 #pragma unroll
                 for (int qq = 0; qq < PP; qq++) {
-                    const int pi = 16 * (q0 + qq) + pl;
-                    const int p = p0 + pi;
-                    const size_t off = (size_t)((pi < n && p != pos) ? p : 0) * KVD + j * HD + dl * 8;
+                    const size_t off = (size_t)kv_row(ksp, 16 * (q0 + qq) + pl, pos) * KVD + j * HD + dl * 8;
                     kk[qq] = *reinterpret_cast<const uint4*>(Ly.kc + off);
                     vv[qq] = *reinterpret_cast<const uint4*>(Ly.vc + off);
                 }
@@ -1271,6 +1287,33 @@ int mdx_persist_k_passes(int n_pos) {
     const int per = (n_pos + GRP - 1) / GRP;
     const int r4 = (per + 63) / 64, r5 = (per + 79) / 80;
     return r4 >= 3 && r5 < r4 ? 5 : 4;
+}
+
+long long mdx_debug_persist_kv_rows(int max_seq, int k_passes, long long* n_checked) {
+    if (max_seq <= 0 || (k_passes != 4 && k_passes != 5)) return -1;
+    const int PP = k_passes;
+    long long bad = 0, cnt = 0;
+    // every position the step can run at, every split, every 16-position
+    // row pl of a pass and every round the kernel requests: the first at
+    // q0 = 0, then (fp16 layers) q0 = PP, 2 PP, ... one at a time, or (int8
+    // and int4 layers) a second set at q0 = PP before the first is computed
+    // and each later one while the previous is computed; all of them are the
+    // rounds q0 = r * PP with 16 * q0 < n, and the first even when n is 0
+    for (int pos = 0; pos < max_seq; pos++)
+        for (int s = 0; s < GRP; s++) {
+            const KvSplit sp = kv_split(pos, s);
+            if (sp.p0 < 0 || (sp.n > 0 && sp.p0 + sp.n > pos + 1)) bad++;
+            for (int q0 = 0; q0 == 0 || 16 * q0 < sp.n; q0 += PP) {
+                for (int qq = 0; qq < PP; qq++)
+                    for (int pl = 0; pl < 16; pl++) {
+                        const int row = kv_row(sp, 16 * (q0 + qq) + pl, pos);
+                        if (row < 0 || row > pos || row >= max_seq) bad++;
+                        cnt++;
+                    }
+            }
+        }
+    if (n_checked) *n_checked = cnt;
+    return bad;
 }
 
 int mdx_persist_debug_poison(void* xbuf, int n_layers, void* stream) {

@@ -132,8 +132,10 @@ struct GemmRound {
 
 // Requests the NKB K-blocks of a round starting at K-block kb (blocks past
 // the wave's range re-read block kb_last; gemm_compute skips them).
+// K need not be a multiple of the K-block: a lane group whose k range lies at
+// or past K (K is a multiple of EPL) loads zero weights and zero activations.
 template <int KIND>
-__device__ __forceinline__ void gemm_issue(GemmRound<KIND>& R, int kb, int kb_last,
+__device__ __forceinline__ void gemm_issue(GemmRound<KIND>& R, int kb, int kb_last, int K,
                                            const uint8_t* const (&wrow)[2], const bool (&wvalid)[2],
                                            const uint16_t* const (&arow)[4], int g) {
     using GK = GemmKind<KIND>;
@@ -141,15 +143,17 @@ __device__ __forceinline__ void gemm_issue(GemmRound<KIND>& R, int kb, int kb_la
 #pragma unroll
     for (int j = 0; j < GK::NKB; j++) {
         const int k = min(kb + j, kb_last) * KB + g * EPL;
+        const bool kin = k < K;
 #pragma unroll
         for (int t = 0; t < 2; t++)
-            R.bw[j][t] = wvalid[t] ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
-                                   : make_uint4(0u, 0u, 0u, 0u);
+            R.bw[j][t] = (wvalid[t] && kin) ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
+                                            : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int r = 0; r < 4; r++)
 #pragma unroll
             for (int s = 0; s < EPL / 8; s++)
-                R.av[j][r][s] = *reinterpret_cast<const uint4*>(arow[r] + k + 8 * s);
+                R.av[j][r][s] = kin ? *reinterpret_cast<const uint4*>(arow[r] + k + 8 * s)
+                                    : make_uint4(0u, 0u, 0u, 0u);
     }
 }
 
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm(const uint1
     const int g = lane >> 4, c16 = lane & 15;
     const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
     // this block's K-blocks (split blockIdx.y of gridDim.y), then this wave's: [kb0, kb1)
-    const int nkb_all = K / KB;
+    const int nkb_all = (K + KB - 1) / KB;   // the last K-block may be partial
     const int per_split = (nkb_all + gridDim.y - 1) / gridDim.y;
     const int sb0 = min(nkb_all, (int)blockIdx.y * per_split);
     const int sb1 = min(nkb_all, sb0 + per_split);
@@ -292,13 +296,13 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm(const uint1
         GemmRound<KIND> r[DP];
 #pragma unroll
         for (int d = 0; d < DP - 1; d++)
-            if (kb0 + d * GK::NKB < kb1) gemm_issue<KIND>(r[d], kb0 + d * GK::NKB, kb1 - 1, wrow, wvalid, arow, g);
+            if (kb0 + d * GK::NKB < kb1) gemm_issue<KIND>(r[d], kb0 + d * GK::NKB, kb1 - 1, K, wrow, wvalid, arow, g);
         for (int kb = kb0; kb < kb1; kb += DP * GK::NKB) {
 #pragma unroll
             for (int d = 0; d < DP; d++) {
                 // request the round DP-1 ahead into the buffer freed last, then multiply round d
                 const int ki = kb + (d + DP - 1) * GK::NKB;
-                if (ki < kb1) gemm_issue<KIND>(r[(d + DP - 1) % DP], ki, kb1 - 1, wrow, wvalid, arow, g);
+                if (ki < kb1) gemm_issue<KIND>(r[(d + DP - 1) % DP], ki, kb1 - 1, K, wrow, wvalid, arow, g);
                 if (kb + d * GK::NKB < kb1) gemm_compute<KIND>(r[d], kb + d * GK::NKB, kb1, acc);
             }
         }
@@ -337,7 +341,7 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm_p(const uin
     const int swiglu = epi == 2;
     const int g = lane >> 4, c16 = lane & 15;
     const size_t row_bytes = KIND == MDX_W_F16 ? (size_t)K * 2 : (KIND == MDX_W_I8 ? (size_t)K : (size_t)K / 2);
-    const int nkb_all = K / KB;
+    const int nkb_all = (K + KB - 1) / KB;   // the last K-block may be partial
     const int per_split = (nkb_all + gridDim.y - 1) / gridDim.y;
     const int sb0 = min(nkb_all, (int)blockIdx.y * per_split);
     const int sb1 = min(nkb_all, sb0 + per_split);
@@ -361,8 +365,8 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm_p(const uin
             const int k = (kb < kb0 ? kb0 : kb) * KB + g * EPL;
 #pragma unroll
             for (int t = 0; t < 2; t++)
-                bw[j][t] = (wvalid[t] && kb0 + j < kb1) ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
-                                                       : make_uint4(0u, 0u, 0u, 0u);
+                bw[j][t] = (wvalid[t] && kb0 + j < kb1 && k < K) ? ld_w(wrow[t] + (size_t)k * 16 / EPL)
+                                                                 : make_uint4(0u, 0u, 0u, 0u);
         }
     }
     float sc_a = 1.0f, sc_b = 1.0f;
@@ -378,7 +382,9 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm_p(const uin
             sc_a = scale[tile * kNT + col];
         }
     }
-    // the panel: 64 rows (rows >= M repeat row M-1) x this split's K range
+    // the panel: 64 rows (rows >= M repeat row M-1) x this split's K range;
+    // columns at or past K (a partial last K-block) are staged as zeros.  The
+    // host never launches an empty split, so cpr >= 1.
     const int ks0 = sb0 * KB, kw = (sb1 - sb0) * KB;
     {
         constexpr int PER = kMaxM * (kPanelK / 8) / (NW * 64);
@@ -390,8 +396,9 @@ __global__ __launch_bounds__(GemmKind<KIND>::WAVES * 64) void k_gemm_p(const uin
             const int c = tid + i * NW * 64;
             const int row = c / cpr, col = c % cpr;
             const int rr = row < M ? row : M - 1;
-            v[i] = row < kMaxM ? *reinterpret_cast<const uint4*>(x16 + (size_t)rr * K + ks0 + 8 * col)
-                               : make_uint4(0u, 0u, 0u, 0u);
+            v[i] = (row < kMaxM && ks0 + 8 * col < K)
+                       ? *reinterpret_cast<const uint4*>(x16 + (size_t)rr * K + ks0 + 8 * col)
+                       : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int i = 0; i < PER; i++) {
@@ -884,20 +891,43 @@ static int gemm_tiles(int N, int swiglu) {
     return swiglu ? (N / 2 + kNT / 2 - 1) / (kNT / 2) : (N + kNT - 1) / kNT;
 }
 
+// K per K-block of k_gemm / k_gemm_p (4 lane groups of one 16-byte load).
+static int gemm_kblock(int kind) { return kind == MDX_W_F16 ? 32 : (kind == MDX_W_I8 ? 64 : 128); }
+
 // K splits of a residual projection: about 256 blocks in all, at least two
-// K-blocks of the widest kind per split.
-static int residual_splits(int N, int K) {
+// K-blocks of the widest kind per split.  The count is then reduced so that
+// no split is empty: the kernels give split s the K-blocks
+// [s * per, (s + 1) * per) with per = ceil(nkb / ns), and every split's
+// consumer sums exactly ns partials.
+static int residual_splits(int kind, int N, int K) {
     const int tiles = gemm_tiles(N, 0);
     int ns = (256 + tiles - 1) / tiles;
     const int max_ns = K / 256 > 0 ? K / 256 : 1;
     if (ns > max_ns) ns = max_ns;
     if (ns > kMaxSplits) ns = kMaxSplits;
-    return ns < 1 ? 1 : ns;
+    if (ns < 1) ns = 1;
+    const int kb = gemm_kblock(kind), nkb = (K + kb - 1) / kb;
+    if (ns > nkb) ns = nkb;
+    const int per = (nkb + ns - 1) / ns;
+    return (nkb + per - 1) / per;
+}
+
+int mdx_debug_gemm_splits(int kind, int N, int K, int* per_split) {
+    if (kind < MDX_W_F16 || kind > MDX_W_I4 || N <= 0 || K <= 0) return -1;
+    const int ns = residual_splits(kind, N, K);
+    const int kb = gemm_kblock(kind), nkb = (K + kb - 1) / kb;
+    if (per_split) *per_split = (nkb + ns - 1) / ns;
+    return ns;
 }
 
 size_t mdx_gemm_scratch_floats(int M, int N, int K) {
     (void)M;
-    const size_t a = (size_t)residual_splits(N, K) * kMaxM * N;
+    int nsm = 1;
+    for (int kind = MDX_W_F16; kind <= MDX_W_I4; kind++) {
+        const int ns = residual_splits(kind, N, K);
+        if (ns > nsm) nsm = ns;
+    }
+    const size_t a = (size_t)nsm * kMaxM * N;
     const size_t b = K % kKS == 0 ? (size_t)(K / kKS) * kMaxM * N : 0;
     return a > b ? a : b;
 }
@@ -911,8 +941,10 @@ static int g_gemm_rounds = 0;
 
 static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilogue, void* out,
                        float* part, int ns, void* stream) {
-    const int kb = w->kind == MDX_W_F16 ? 32 : (w->kind == MDX_W_I8 ? 64 : 128);
-    if (M <= 0 || M > kMaxM || w->K % kb != 0) return -1;
+    if (w->kind < MDX_W_F16 || w->kind > MDX_W_I4) return -5;
+    const int kb = gemm_kblock(w->kind);
+    // K a multiple of one lane group's 16-byte load (the last K-block may be partial)
+    if (M <= 0 || M > kMaxM || w->K <= 0 || w->K % (kb / 4) != 0) return -1;
     // exactly one destination: split partials, or the epilogue's output
     if (part ? (ns < 1 || out != nullptr) : (ns != 1 || out == nullptr)) return -1;
     if (epilogue == 2 && w->N % 2) return -1;
@@ -928,7 +960,8 @@ static int gemm_launch(const uint16_t* x16, int M, const mdx_wdesc* w, int epilo
     // int8 9.23 -> 8.96, int4 9.03 -> 8.46) and, with fp16 weights, for split
     // partials (qkv, two splits of 512: 7.42 -> 7.33 us; int8 and int4 6.03 ->
     // 6.39 and 6.01 -> 6.20, so those keep k_gemm).
-    const int nkb = w->K / kb, per_split = (nkb + ns - 1) / ns;
+    const int nkb = (w->K + kb - 1) / kb, per_split = (nkb + ns - 1) / ns;
+    if ((ns - 1) * per_split >= nkb) return -1;   // an empty split
     const bool panel = per_split * kb <= kPanelK && (epilogue == 2 || w->kind == MDX_W_F16);
     if (panel && !g_gemm_rounds) {
         switch (w->kind) {
@@ -988,7 +1021,7 @@ int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w
         ns = w->K / kKS;
         rc = gemm_s_launch(x16, M, w, scratch, stream);
     } else {
-        ns = residual_splits(w->N, w->K);
+        ns = residual_splits(w->kind, w->N, w->K);
         rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
     }
     if (rc) return rc;
@@ -1018,7 +1051,7 @@ int mdx_launch_qkv_rope_append_rows(const uint16_t* x16, int M, const mdx_wdesc*
                                     int hd, int rope_style, float* q_out, uint16_t* k_cache,
                                     uint16_t* v_cache, void* stream) {
     if (hd % 2 || hd > 2 * 64 * kRopePairs || M <= 0 || w->N != (nq + 2 * nkv) * hd) return -1;
-    const int ns = residual_splits(w->N, w->K);
+    const int ns = residual_splits(w->kind, w->N, w->K);
     int rc = gemm_launch(x16, M, w, 0, nullptr, scratch, ns, stream);
     if (rc) return rc;
     hipLaunchKernelGGL(k_qk_rope_append_rows, dim3(nq + 2 * nkv, M), dim3(64), 0, (hipStream_t)stream,

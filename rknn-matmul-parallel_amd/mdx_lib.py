@@ -146,6 +146,8 @@ def lib() -> C.CDLL:
             "mdx_device_synchronize": (C.c_int, []),
             "mdx_debug_gemv": (C.c_int, [C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
             "mdx_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F]),
+            "mdx_debug_gemm_splits": (C.c_int, [C.c_int, C.c_int, C.c_int, _I]),
+            "mdx_debug_persist_kv_rows": (C.c_longlong, [C.c_int, C.c_int, C.POINTER(C.c_longlong)]),
             "mdx_debug_gemm_residual": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, P, _F, _F, _F,
                                                   _F, C.c_float, C.POINTER(C.c_uint16)]),
             "mdx_debug_attn_decode": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,

@@ -96,7 +96,7 @@ def test_gemv_fp32_activation_rows(mdx, gpu, oracle_lib):
 
 @pytest.mark.parametrize("kind", [0, 1, 2])
 @pytest.mark.parametrize("M,K,N", [(60, 1024, 4096), (60, 3072, 1024), (1, 1024, 1024),
-                                   (64, 2048, 1024), (7, 1024, 6144)])
+                                   (64, 2048, 1024), (7, 1024, 6144), (64, 352, 96), (3, 96, 64)])
 def test_gemm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
     rng = np.random.default_rng(M * 31 + K + N + kind)
     x = rng.standard_normal((M, K)).astype(np.float32)
@@ -115,15 +115,15 @@ def test_gemm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
 # order grouped per XCD (N/64 x K/256 a multiple of 8: (60,2048,1024),
 # (60,3072,1024), (5,4096,192), (33,1024,4096)), the plain order otherwise
 # ((17,768,960): 45 blocks; (64,256,64): one block), and K not a multiple of
-# 256 (the k_gemm path: (9,320,128)).  hidden += x.W*s is checked against the
-# oracle's projection; the fp16 normed rows against numpy on the returned
-# hidden (one fp16 ulp).
+# 256 (the k_gemm path: (9,320,128), whose last K-block is partial for int8
+# and int4, and (11,2592,128), where ten requested splits of 81 fp16
+# K-blocks would leave the last one empty).  hidden += x.W*s is checked
+# against the oracle's projection; the fp16 normed rows against numpy on the
+# returned hidden (one fp16 ulp).
 @pytest.mark.parametrize("kind", [0, 1, 2])
 @pytest.mark.parametrize("M,K,N", [(60, 2048, 1024), (60, 3072, 1024), (5, 4096, 192), (33, 1024, 4096),
-                                   (17, 768, 960), (64, 256, 64), (9, 320, 128)])
+                                   (17, 768, 960), (64, 256, 64), (9, 320, 128), (11, 2592, 128)])
 def test_gemm_residual_norm_matches_oracle(mdx, gpu, oracle_lib, kind, M, K, N):
-    if kind == 2 and K % 128:
-        pytest.skip("int4 projections take K in multiples of 128")
     rng = np.random.default_rng(M * 7 + K * 3 + N + kind)
     x = rng.standard_normal((M, K)).astype(np.float32)
     if kind == 0:

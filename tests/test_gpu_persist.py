@@ -490,3 +490,66 @@ def test_step_sample_after_one_launch_step(mdx, gpu, oracle_lib, models):
     assert a.seq_len == b.seq_len == 48
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("quant", [0, 1])
+def test_reference_python_callers_call_sequences(mdx, gpu, oracle_lib, models, quant):
+    """The two reference Python callers' call sequences through the pybind
+    module, on the one-launch path, against the oracle:
+    - python/matmul_decoder.py:196-203 (run_embed): step_get_token(token_id=-1,
+      embedding=row) for every embedding row, then step_get_token(token_id=-1,
+      embedding=None), which the reference's C step rejects (no embedding and
+      token -1: src/matmul_decoder.c:1447-1452), so the module returns -1 and
+      the cache does not advance;
+    - examples/qwen3_asr/matmul_decoder.py:186-201 (run_embed):
+      prefill(token_id=-1, embedding=row) for all rows but the last (a step
+      without the lm_head), step_get_token(token_id=-1, embedding=last row),
+      then step_get_token(token_id=prev) fed back for the generated tokens.
+    The oracle runs the same calls, fed the tokens the module returned (the
+    caller's own feedback), and every returned token is the oracle's argmax
+    for that step, or within the step tests' logit bar of it (2e-3 of the
+    largest |logit|: a near tie, where two valid accumulation orders may
+    pick either)."""
+    import matmul_decoder as md     # the pybind module, beside mdx_lib on the test path
+    cfg, get = models
+    path = get(quant)
+    dec = md.MatmulDecoder(path, max_seq_len=256, quant_type=QUANTS[quant])
+    rng = np.random.default_rng(77 + quant)
+    n = 6
+    emb = (rng.standard_normal((n, SHAPE["hidden_dim"])) * 0.5).astype(np.float32)
+
+    # python/matmul_decoder.py: every row through step_get_token
+    def same_choice(t, to, lo, what):
+        assert 0 <= t < SHAPE["vocab_size"], what
+        assert t == to or lo[to] - lo[t] <= 2e-3 * float(np.abs(lo).max()), f"{what}: {t} vs {to}"
+
+    dec.clear_kv_cache()
+    o = oracle_lib.Model(path, SHAPE, quant, 256, kv_fp16=True)
+    for i in range(n):
+        t = dec.step_get_token(token_id=-1, embedding=emb[i])
+        to, lo = o.step(-1, emb[i])
+        same_choice(t, to, lo, f"row {i}")
+    assert dec.seq_len == n
+    for _ in range(3):
+        assert dec.step_get_token(token_id=-1, embedding=None) == -1
+        assert o.step(-1, None)[0] == -1
+    assert dec.seq_len == n and o.seq_len == n
+
+    # examples/qwen3_asr/matmul_decoder.py: prefill rows, last row with the head, then greedy
+    dec.clear_kv_cache()
+    o = oracle_lib.Model(path, SHAPE, quant, 256, kv_fp16=True)
+    for i in range(n - 1):
+        dec.prefill(token_id=-1, embedding=emb[i])
+        o.step(-1, emb[i], logits=False)
+    first = dec.step_get_token(token_id=-1, embedding=emb[n - 1])
+    to, lo = o.step(-1, emb[n - 1])
+    same_choice(first, to, lo, "first token")
+    prev, exact = first, int(first == to)
+    for i in range(12):
+        t = dec.step_get_token(token_id=prev)
+        to, lo = o.step(prev)
+        same_choice(t, to, lo, f"generated token {i + 1}")
+        exact += int(t == to)
+        prev = t
+    assert exact >= 11, f"only {exact} of 13 tokens equal to the oracle's argmax"
+    assert dec.seq_len == n + 12

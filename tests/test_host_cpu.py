@@ -207,3 +207,43 @@ def test_sampler_parameter_checks_run_before_any_device_call(mdx):
         assert call(**kw) == -1, kw
     assert call(u=1.01) == -1 and call(u=-0.01) == -1
     assert call(top_k=1000, top_p=0.9, temperature=0.7, repeat_tokens=[1, 1, 2], repeat_penalty=1.3) == -5
+
+
+def test_gemm_splits_are_never_empty(mdx):
+    """The K-split count of a split prefill projection (host arithmetic,
+    mdx_debug_gemm_splits) leaves no split empty for any kind and shape the
+    config check admits (K, N multiples of 32 up to 16384), the case where
+    an empty split once reached the kernels (fp16 K=2592, N=128: 81
+    K-blocks, 10 requested splits of 9) included."""
+    import ctypes
+    L = mdx.lib()
+    per = ctypes.c_int(0)
+    blocks = {0: 32, 1: 64, 2: 128}
+    checked = 0
+    for kind, kb in blocks.items():
+        for K in list(range(32, 4097, 32)) + [6144, 8192, 12288, 16384]:
+            for N in (32, 64, 96, 128, 160, 192, 256, 480, 1024, 2048, 4096, 6144):
+                ns = L.mdx_debug_gemm_splits(kind, N, K, ctypes.byref(per))
+                nkb = -(-K // kb)
+                assert 1 <= ns <= 16, (kind, K, N, ns)
+                assert per.value == -(-nkb // ns), (kind, K, N)
+                assert (ns - 1) * per.value < nkb, f"empty split: kind {kind} K {K} N {N} ns {ns}"
+                assert ns * per.value >= nkb
+                checked += 1
+    assert L.mdx_debug_gemm_splits(0, 128, 2592, ctypes.byref(per)) == 9 and per.value == 9
+    assert L.mdx_debug_gemm_splits(5, 128, 256, None) == -1
+    assert checked > 4000
+
+
+def test_persist_kv_rows_stay_in_the_written_cache(mdx):
+    """Every K/V row address the one-launch decode step forms (the kernel's
+    own kv_split / kv_row functions, enumerated on the host over every
+    position of a 6400-row cache, every split, pass row and requested round,
+    for rounds of 4 and of 5 passes) lies in rows [0, pos]."""
+    import ctypes
+    L = mdx.lib()
+    n = ctypes.c_longlong(0)
+    for pp in (4, 5):
+        assert L.mdx_debug_persist_kv_rows(6400, pp, ctypes.byref(n)) == 0, pp
+        assert n.value > 6400 * 32 * 16 * pp
+    assert L.mdx_debug_persist_kv_rows(100, 3, None) == -1
