@@ -564,7 +564,41 @@ static int run_head(MatmulDecoderContext* c, const mdx_wdesc* lm, int* out_token
  * and the FFN half, each starting from the other's K-split partials (the
  * residual rows alternate between two buffers); after the last layer the
  * down partials are added to the residual rows without a norm. */
+/* Plain mode of the same launches: each half reads fp16 normed rows written
+ * by the split-sum/residual/RMSNorm kernel before it (four launches per
+ * layer). */
+static int run_prefill_xg_plain(MatmulDecoderContext* c, int M, void* s) {
+    const float eps = c->config.rms_eps;
+    float* P = c->d_xg_part;
+    mdx_prefill_xg_args a;
+    memset(&a, 0, sizeof a);
+    a.x16 = c->d_bx16;
+    a.state = c->d_state;
+    a.M = M;
+    a.n_layers = c->L;
+    a.eps = eps;
+    a.part_out = P;
+    a.xbuf = c->d_xg;
+    a.trace = c->xg_trace;
+    int rc = mdx_launch_rmsnorm_rows(c->d_bhidden, c->layers[0].in_norm, eps, M, c->d, c->d_bx16, s);
+    for (int l = 0; l < c->L && rc == 0; l++) {
+        md_layer* ly = &c->layers[l];
+        const float* next_norm = l + 1 < c->L ? c->layers[l + 1].in_norm : NULL;
+        a.layer = l;
+        rc = mdx_launch_prefill_attn(&a, &ly->qkv, &ly->o, ly->q_norm, ly->k_norm, c->d_cos, c->d_sin,
+                                     c->config.rope_style, ly->kc, ly->vc, s);
+        if (!rc)
+            rc = mdx_launch_residual_norm(P, 8, M, c->d, ly->o.scale, c->d_bhidden, ly->post_norm, eps, c->d_bx16, s);
+        if (!rc) rc = mdx_launch_prefill_mlp(&a, &ly->gu, &ly->down, s);
+        if (!rc)
+            rc = mdx_launch_residual_norm(P, 8, M, c->d, ly->down.scale, c->d_bhidden, next_norm, eps, c->d_bx16, s);
+    }
+    if (!rc) rc = mdx_launch_prefill_xg_end(c->d_state, M, c->d_xg, s);
+    return rc;
+}
+
 static int run_prefill_xg(MatmulDecoderContext* c, int M, void* s) {
+    if (getenv("MDX_XG_PLAIN")) return run_prefill_xg_plain(c, M, s);
     float* H[2] = {c->d_bhidden, c->d_xg_h2};
     float* Po = c->d_xg_part;
     float* Pd = c->d_xg_part + (size_t)8 * 64 * c->d;

@@ -262,6 +262,9 @@ size_t mdx_prefill_xg_buf_bytes(void);
  * RMSNorm norm_w; then the half's projections, whose 8 K-split partials go to
  * part_out (which must differ from part_in). */
 typedef struct {
+    const uint16_t* x16;           /* plain mode when not NULL: the launch's normed input
+                                      rows [M][1024] fp16 (no N stage; h_in, h_out,
+                                      part_in, scale_in and norm_w are not used) */
     const mdx_state* state;
     int M, n_layers, layer;
     float eps;

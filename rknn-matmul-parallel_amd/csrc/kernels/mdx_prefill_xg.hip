@@ -251,6 +251,7 @@ __device__ __forceinline__ bool stage_ll_panel(uint4* panel, __amdgpu_buffer_rsr
 }
 
 struct XgArgs {
+    const uint16_t* x16;      // plain mode: [M][1024] fp16 normed input rows (no N stage), else NULL
     const mdx_state* st;
     int M, n_layers, layer, rope_style;
     float eps;
@@ -287,6 +288,24 @@ struct XgArgs {
 // Thread t owns columns 4 (t & 255) .. +3 of row 2c + (t >> 8).  Split in two
 // so that the partials are requested before the stage's weights: nload issues
 // every load, nfinish uses them.
+// Plain mode: stages x16[row][k0 .. k0 + 256) (rows >= M as zeros) into an LDS
+// panel of PITCH uint4 per row: 4 uint4 per thread, all requested together.
+template <int PITCH>
+__device__ __forceinline__ void stage_plain256(uint4* panel, const uint16_t* x16, int M, int k0, int t) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = t + NT * i, row = q >> 5, col = q & 31;
+        v[i] = row < M ? *reinterpret_cast<const uint4*>(x16 + (size_t)row * D + k0 + 8 * col)
+                       : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = t + NT * i;
+        panel[(q >> 5) * PITCH + (q & 31)] = v[i];
+    }
+}
+
 struct NRows {
     float4 h, p[8], sc, nw;
 };
@@ -380,8 +399,9 @@ __global__ __launch_bounds__(NT) void k_prefill_attn(XgArgs a) {
     };
     const int l4 = lane >> 4, c16 = lane & 15;
     XG_TRACE(0, 0);
+    const bool plain = a.x16 != nullptr;
     NRows nr_;
-    stage_norm_load(a, c, t, nr_);
+    if (!plain) stage_norm_load(a, c, t, nr_);
     // stage R's operands: its head slot's column scales and norm weights, and
     // the RoPE table entries of its row (positions start + row)
     const int rh = c & 3, rrow = 8 * (c >> 2) + wave;
@@ -410,7 +430,7 @@ __global__ __launch_bounds__(NT) void k_prefill_attn(XgArgs a) {
     XG_TRACE(0, 1);
 
     // ================= N =================
-    stage_norm_finish(a, rs, ep_xn, j, c, t, nr_, ss_red);
+    if (!plain) stage_norm_finish(a, rs, ep_xn, j, c, t, nr_, ss_red);
 
     // ---------- the weights of both projections, requested after the N stage's loads
     // have returned (requested earlier they queue in front of them) ----------
@@ -429,7 +449,8 @@ __global__ __launch_bounds__(NT) void k_prefill_attn(XgArgs a) {
     XG_TRACE(0, 2);
 
     // ================= Q =================
-    if (!stage_ll_panel<256, D, PQ>(panel, rs, X_XN, 256 * s, M, ep_xn, dead, lim, t)) { dead = true; timed_out(); }
+    if (plain) stage_plain256<PQ>(panel, a.x16, M, 256 * s, t);
+    else if (!stage_ll_panel<256, D, PQ>(panel, rs, X_XN, 256 * s, M, ep_xn, dead, lim, t)) { dead = true; timed_out(); }
     __syncthreads();
     XG_TRACE(0, 4);
     float4_t acc[4];
@@ -771,8 +792,9 @@ __global__ __launch_bounds__(NT) void k_prefill_mlp(XgArgs a) {
     };
     const int l4 = lane >> 4, c16 = lane & 15;
     XG_TRACE(1, 0);
+    const bool plain = a.x16 != nullptr;
     NRows nr_;
-    stage_norm_load(a, c, t, nr_);
+    if (!plain) stage_norm_load(a, c, t, nr_);
     // S's column scales
     const int srow = 2 * c + t / 192, sfp = 2 * (t % 192);
     float sg[2] = {1.f, 1.f}, su[2] = {1.f, 1.f};
@@ -786,7 +808,7 @@ __global__ __launch_bounds__(NT) void k_prefill_mlp(XgArgs a) {
     XG_TRACE(1, 1);
 
     // ================= N =================
-    stage_norm_finish(a, rs, ep_xn, j, c, t, nr_, ss_red);
+    if (!plain) stage_norm_finish(a, rs, ep_xn, j, c, t, nr_, ss_red);
 
     // G: tile group pg (48 features: gate tiles 0..2, up tiles 3..5), K split s
     const int pg = c & 7, s = c >> 3;
@@ -804,7 +826,8 @@ __global__ __launch_bounds__(NT) void k_prefill_mlp(XgArgs a) {
     XG_TRACE(1, 2);
 
     // ================= G =================
-    if (!stage_ll_panel<256, D, PQ>(panel, rs, X_XN, 256 * s, M, ep_xn, dead, lim, t)) { dead = true; timed_out(); }
+    if (plain) stage_plain256<PQ>(panel, a.x16, M, 256 * s, t);
+    else if (!stage_ll_panel<256, D, PQ>(panel, rs, X_XN, 256 * s, M, ep_xn, dead, lim, t)) { dead = true; timed_out(); }
     __syncthreads();
     XG_TRACE(1, 4);
     float4_t acc[4];
@@ -929,11 +952,14 @@ size_t mdx_prefill_xg_buf_bytes(void) { return X_BYTES; }
 int mdx_launch_prefill_attn(const mdx_prefill_xg_args* p, const mdx_wdesc* qkv, const mdx_wdesc* o,
                             const float* q_norm, const float* k_norm, const float* cos_t, const float* sin_t,
                             int rope_style, uint16_t* k_cache, uint16_t* v_cache, void* stream) {
-    if (!p || p->M <= 0 || p->M > MR || !p->state || !p->h_in || !p->h_out || !p->norm_w || !p->part_out ||
-        !p->xbuf || !qkv || !o || qkv->kind != o->kind || qkv->K != D || qkv->N != QD + 2 * KVD || o->K != QD ||
-        o->N != D || p->layer < 0 || p->layer >= p->n_layers || p->part_in == p->part_out || p->h_in == p->h_out)
+    const bool plain = p && p->x16;
+    if (!p || p->M <= 0 || p->M > MR || !p->state || !p->part_out || !p->xbuf || !qkv || !o ||
+        qkv->kind != o->kind || qkv->K != D || qkv->N != QD + 2 * KVD || o->K != QD || o->N != D || p->layer < 0 ||
+        p->layer >= p->n_layers ||
+        (!plain && (!p->h_in || !p->h_out || !p->norm_w || p->part_in == p->part_out || p->h_in == p->h_out)))
         return -1;
     XgArgs a = {};
+    a.x16 = p->x16;
     a.st = p->state;
     a.M = p->M;
     a.n_layers = p->n_layers;
@@ -962,12 +988,15 @@ int mdx_launch_prefill_attn(const mdx_prefill_xg_args* p, const mdx_wdesc* qkv, 
 
 int mdx_launch_prefill_mlp(const mdx_prefill_xg_args* p, const mdx_wdesc* gu, const mdx_wdesc* down,
                            void* stream) {
-    if (!p || p->M <= 0 || p->M > MR || !p->state || !p->h_in || !p->h_out || !p->norm_w || !p->part_in ||
-        !p->part_out || !p->xbuf || !gu || !down || gu->kind != down->kind || gu->K != D || gu->N != 2 * FF ||
-        down->K != FF || down->N != D || p->layer < 0 || p->layer >= p->n_layers || p->part_in == p->part_out ||
-        p->h_in == p->h_out)
+    const bool plain = p && p->x16;
+    if (!p || p->M <= 0 || p->M > MR || !p->state || !p->part_out || !p->xbuf || !gu || !down ||
+        gu->kind != down->kind || gu->K != D || gu->N != 2 * FF || down->K != FF || down->N != D || p->layer < 0 ||
+        p->layer >= p->n_layers ||
+        (!plain && (!p->h_in || !p->h_out || !p->norm_w || !p->part_in || p->part_in == p->part_out ||
+                    p->h_in == p->h_out)))
         return -1;
     XgArgs a = {};
+    a.x16 = p->x16;
     a.st = p->state;
     a.M = p->M;
     a.n_layers = p->n_layers;
