@@ -46,31 +46,6 @@ int mdx_copy_probe(size_t bytes, int iters);
  * again as a cooperative launch, and the context keeps launching
  * cooperatively. */
 int mdx_decode_path(const MatmulDecoderContext* ctx);
-/* Which path the next batch-prefill chunk takes:
- *   1  two launches per layer (the 0.6B layer shape with one weight kind for
- *      all projections, up to 1024 cached positions after the chunk): the
- *      attention half and the FFN half, each starting from the other's
- *      K-split partials (summed with the residual and the RMSNorm);
- *   0  eight launches per layer (any shape).
- * MDX_PREFILL_XG=0 in the environment at creation selects 0.  If a wait of
- * the two-launch path times out (its workgroups are not co-located as it
- * relies on), the chunk runs again on the eight-launch path and the context
- * stays on it. */
-int mdx_prefill_path(const MatmulDecoderContext* ctx);
-/* Test hook: -1 the default choice above, 0 / 1 force the eight- / two-launch
- * prefill (1 returns MATMUL_DECODER_ERR_UNSUPPORTED for a model it cannot
- * serve).  Takes effect for the next chunk (graphs are kept per path). */
-int mdx_debug_prefill_xg(MatmulDecoderContext* ctx, int mode);
-/* Test hook: the two-launch prefill's waits give up after `rounds` polls
- * (0: the default limit), for every chunk until set again. */
-int mdx_debug_prefill_xg_spin(MatmulDecoderContext* ctx, unsigned rounds);
-/* One two-launch prefill chunk of M rows (as matmul_decoder_prefill_batch,
- * launched eagerly) with per-workgroup timestamps of the 100 MHz device clock
- * at its stage boundaries: out[n_layers][2][256][16] (cap >= that many
- * values; unused events are 0).  Returns 16 (events per workgroup and launch),
- * MATMUL_DECODER_ERR_UNSUPPORTED when the chunk would not take that path. */
-int mdx_trace_prefill(MatmulDecoderContext* ctx, const float* embeddings, int M, unsigned long long* out,
-                      size_t cap);
 /* Test hook: the next one-launch step polls each exchange at most `rounds`
  * times before giving up (0: the default), which forces the timeout-and-retry
  * path without any workgroup waiting long. */

@@ -30,7 +30,6 @@ typedef struct {
 
 typedef struct {
     int M;
-    int xg;                  /* 1: captured on the two-launch (fused) path */
     void* exec;
 } md_pgraph;
 
@@ -83,15 +82,6 @@ struct MatmulDecoderContext {
                                 uncached words serve the others (or NULL) */
     int lx_off;              /* set after a timed-out step: per-head exchanges through xbuf */
     int lx_force;            /* test hook: -1 default, 0 / 1 force them off / on */
-    void* d_xg;              /* exchange words of the two-launch prefill (or NULL) */
-    float* d_xg_h2;          /* its second buffer of residual rows [64][d] */
-    float* d_xg_part;        /* its o and down K-split partials [2][8][64][d] */
-    int xg_ok;               /* 1: the two-launch prefill serves this model */
-    int xg_off;              /* set after one of its waits timed out: eight launches from then on */
-    int xg_force;            /* test hook: -1 default, 0 / 1 force it off / on */
-    unsigned xg_runs;        /* chunks run on it since its words were last cleared */
-    unsigned long long* xg_trace;  /* set only during mdx_trace_prefill */
-    int capture_xg;
     mdx_persist_args pargs;
     mdx_state* h_state;
     float* h_io;
@@ -387,11 +377,6 @@ static int layout(MatmulDecoderContext* c, const md_source* s) {
     CARVE(c->d_act16, (size_t)c->F * 2);
     CARVE(c->d_partial, mdx_lmhead_scratch_bytes());
     CARVE(c->d_xbuf, mdx_persist_xbuf_bytes());
-    if (mdx_prefill_xg_shape_ok(c->d, c->nq, c->nkv, c->hd, c->F)) {
-        CARVE(c->d_xg, mdx_prefill_xg_buf_bytes());
-        CARVE(c->d_xg_h2, (size_t)64 * c->d * 4);
-        CARVE(c->d_xg_part, (size_t)2 * 8 * 64 * c->d * 4);
-    }
     const int mm = c->max_m;
     const int kmax = c->F > c->qd ? (c->F > c->d ? c->F : c->d) : (c->qd > c->d ? c->qd : c->d);
     CARVE(c->d_bhidden, (size_t)mm * c->d * 4);
@@ -560,97 +545,7 @@ static int run_head(MatmulDecoderContext* c, const mdx_wdesc* lm, int* out_token
                              c->d_partial, c->d_state, out_tokens, advance, s);
 }
 
-/* The two-launch prefill (mdx_prefill_xg.hip): per layer the attention half
- * and the FFN half, each starting from the other's K-split partials (the
- * residual rows alternate between two buffers); after the last layer the
- * down partials are added to the residual rows without a norm. */
-/* Plain mode of the same launches: each half reads fp16 normed rows written
- * by the split-sum/residual/RMSNorm kernel before it (four launches per
- * layer). */
-static int run_prefill_xg_plain(MatmulDecoderContext* c, int M, void* s) {
-    const float eps = c->config.rms_eps;
-    float* P = c->d_xg_part;
-    mdx_prefill_xg_args a;
-    memset(&a, 0, sizeof a);
-    a.x16 = c->d_bx16;
-    a.state = c->d_state;
-    a.M = M;
-    a.n_layers = c->L;
-    a.eps = eps;
-    a.part_out = P;
-    a.xbuf = c->d_xg;
-    a.trace = c->xg_trace;
-    int rc = mdx_launch_rmsnorm_rows(c->d_bhidden, c->layers[0].in_norm, eps, M, c->d, c->d_bx16, s);
-    for (int l = 0; l < c->L && rc == 0; l++) {
-        md_layer* ly = &c->layers[l];
-        const float* next_norm = l + 1 < c->L ? c->layers[l + 1].in_norm : NULL;
-        a.layer = l;
-        rc = mdx_launch_prefill_attn(&a, &ly->qkv, &ly->o, ly->q_norm, ly->k_norm, c->d_cos, c->d_sin,
-                                     c->config.rope_style, ly->kc, ly->vc, s);
-        if (!rc)
-            rc = mdx_launch_residual_norm(P, 8, M, c->d, ly->o.scale, c->d_bhidden, ly->post_norm, eps, c->d_bx16, s);
-        if (!rc) rc = mdx_launch_prefill_mlp(&a, &ly->gu, &ly->down, s);
-        if (!rc)
-            rc = mdx_launch_residual_norm(P, 8, M, c->d, ly->down.scale, c->d_bhidden, next_norm, eps, c->d_bx16, s);
-    }
-    if (!rc) rc = mdx_launch_prefill_xg_end(c->d_state, M, c->d_xg, s);
-    return rc;
-}
-
-static int run_prefill_xg(MatmulDecoderContext* c, int M, void* s) {
-    if (getenv("MDX_XG_PLAIN")) return run_prefill_xg_plain(c, M, s);
-    float* H[2] = {c->d_bhidden, c->d_xg_h2};
-    float* Po = c->d_xg_part;
-    float* Pd = c->d_xg_part + (size_t)8 * 64 * c->d;
-    mdx_prefill_xg_args a;
-    memset(&a, 0, sizeof a);
-    a.state = c->d_state;
-    a.M = M;
-    a.n_layers = c->L;
-    a.eps = c->config.rms_eps;
-    a.xbuf = c->d_xg;
-    a.trace = c->xg_trace;
-    int rc = 0, cur = 0;
-    for (int l = 0; l < c->L && rc == 0; l++) {
-        md_layer* ly = &c->layers[l];
-        a.layer = l;
-        a.h_in = H[cur];
-        a.h_out = H[cur ^ 1];
-        a.part_in = l ? Pd : NULL;
-        a.scale_in = l ? c->layers[l - 1].down.scale : NULL;
-        a.norm_w = ly->in_norm;
-        a.part_out = Po;
-        rc = mdx_launch_prefill_attn(&a, &ly->qkv, &ly->o, ly->q_norm, ly->k_norm, c->d_cos, c->d_sin,
-                                     c->config.rope_style, ly->kc, ly->vc, s);
-        cur ^= 1;
-        a.h_in = H[cur];
-        a.h_out = H[cur ^ 1];
-        a.part_in = Po;
-        a.scale_in = ly->o.scale;
-        a.norm_w = ly->post_norm;
-        a.part_out = Pd;
-        if (!rc) rc = mdx_launch_prefill_mlp(&a, &ly->gu, &ly->down, s);
-        cur ^= 1;
-    }
-    /* 2 L swaps: the residual rows are back in d_bhidden */
-    if (!rc)
-        rc = mdx_launch_residual_norm(Pd, 8, M, c->d, c->layers[c->L - 1].down.scale, c->d_bhidden, NULL,
-                                      a.eps, NULL, s);
-    if (!rc) rc = mdx_launch_prefill_xg_end(c->d_state, M, c->d_xg, s);
-    return rc;
-}
-
-/* 1 when the next prefill chunk takes the two-launch path. */
-static int use_xg(const MatmulDecoderContext* c) {
-    if (!c->xg_ok || !c->d_xg) return 0;
-    if (c->xg_force >= 0) return c->xg_force;
-    /* each row attends in rounds of 64 positions from two rows per
-     * workgroup: long contexts go to the eight-launch path's attention */
-    return !c->xg_off && c->seq_len + c->max_m <= 1024;
-}
-
 static int run_prefill(MatmulDecoderContext* c, int M, void* s) {
-    if (use_xg(c)) return run_prefill_xg(c, M, s);
     const float eps = c->config.rms_eps;
     /* the first layer's input norm; every later norm is fused into the
      * residual projection before it */
@@ -719,27 +614,22 @@ static int ensure_graphs(MatmulDecoderContext* c) {
     return 0;
 }
 
-static int seq_prefill(MatmulDecoderContext* c, void* s) {
-    return c->capture_xg ? run_prefill_xg(c, c->capture_M, s) : run_prefill(c, c->capture_M, s);
-}
+static int seq_prefill(MatmulDecoderContext* c, void* s) { return run_prefill(c, c->capture_M, s); }
 
 static void* prefill_graph(MatmulDecoderContext* c, int M) {
     if (!c->use_graphs) return NULL;
-    const int xg = use_xg(c);
     for (int i = 0; i < 4; i++)
-        if (c->pgraphs[i].exec && c->pgraphs[i].M == M && c->pgraphs[i].xg == xg) return c->pgraphs[i].exec;
+        if (c->pgraphs[i].exec && c->pgraphs[i].M == M) return c->pgraphs[i].exec;
     md_pgraph* slot = &c->pgraphs[c->pgraph_next];
     c->pgraph_next = (c->pgraph_next + 1) % 4;
     if (slot->exec) mdxrt_graph_destroy(slot->exec);
     slot->exec = NULL;
     c->capture_M = M;
-    c->capture_xg = xg;
     if (capture(c, seq_prefill, &slot->exec) != 0) {
         slot->exec = NULL;
         return NULL;
     }
     slot->M = M;
-    slot->xg = xg;
     return slot->exec;
 }
 
@@ -1045,15 +935,6 @@ static MatmulDecoderContext* create_common(const MatmulDecoderConfig* config,
         c->profile = e && e[0] == '1';
         c->kv_stream_force = -1;
         c->lx_force = -1;
-        c->xg_force = -1;
-        const char* x = getenv("MDX_PREFILL_XG");
-        int ok = c->d_xg != NULL && !(x && x[0] == '0');
-        for (int l = 0; l < c->L && ok; l++) {
-            const md_layer* ly = &c->layers[l];
-            ok = ly->qkv.kind == ly->o.kind && ly->qkv.kind == ly->gu.kind && ly->qkv.kind == ly->down.kind &&
-                 ly->qkv.kind <= MDX_W_I4;
-        }
-        c->xg_ok = ok;
     }
     if (c->profile && c->persist) {
         c->trace_ev = mdx_persist_trace_events(c->L);
@@ -1432,54 +1313,18 @@ int matmul_decoder_step_head(MatmulDecoderContext* c, int token_id, const float*
     return c->h_state->argmax;
 }
 
-/* The exchange words carry 16-bit epochs that repeat after 65535 prefill
- * counts; words of rows that no recent chunk wrote could then look current.
- * Every 4096 chunks the words are cleared (counter and test words kept). */
-static int xg_refresh(MatmulDecoderContext* c) {
-    if (++c->xg_runs < 4096) return 0;
-    c->xg_runs = 0;
-    const size_t hdr = 64 * 4;
-    return mdxrt_fill_u32((char*)c->d_xg + hdr, 0u, (mdx_prefill_xg_buf_bytes() - hdr) / 4, c->stream);
-}
-
-/* After a two-launch prefill: 1 when one of its waits timed out (its
- * workgroups were not placed as it relies on, e.g. beside another process's
- * grid); the status word is cleared again.  The stream is synchronised. */
-static int xg_timed_out(MatmulDecoderContext* c) {
-    int* st = &c->h_res[2];
-    *st = 0;
-    if (mdxrt_d2h_async(st, (const char*)c->d_xg + 4, 4, c->stream) || mdxrt_stream_sync(c->stream)) return 0;
-    if (!*st) return 0;
-    if (mdxrt_fill_u32((char*)c->d_xg + 4, 0u, 1, c->stream) == 0) mdxrt_stream_sync(c->stream);
-    return 1;
-}
-
 static int prefill_chunk(MatmulDecoderContext* c, const float* emb, int M) {
     memcpy(c->h_io, emb, (size_t)M * c->d * 4);
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
-    const int xg = use_xg(c);
-    /* the two-launch path needs its grid co-resident, as the one-launch step does */
-    if (xg) pthread_mutex_lock(&g_persist_mu);
-    int rc = xg ? xg_refresh(c) : 0;
-    if (!rc) rc = mdxrt_h2d_async(c->d_bhidden, c->h_io, (size_t)M * c->d * 4, c->stream);
+    int rc = mdxrt_h2d_async(c->d_bhidden, c->h_io, (size_t)M * c->d * 4, c->stream);
     if (!rc) rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
     void* g = rc ? NULL : prefill_graph(c, M);
     if (!rc) rc = g ? mdxrt_graph_launch(g, c->stream) : run_prefill(c, M, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
-    const int redo = !rc && xg && xg_timed_out(c);
-    if (xg) pthread_mutex_unlock(&g_persist_mu);
     if (rc) {
         fprintf(stderr, "[BatchPrefill] failed: %s\n", mdxrt_last_error());
         return MATMUL_DECODER_ERR_RKNN;
-    }
-    if (redo) {
-        /* the chunk again, from the same rows, on the eight-launch path */
-        fprintf(stderr, "[BatchPrefill] a wait of the two-launch prefill timed out; "
-                        "running the chunk again with eight launches per layer\n");
-        c->xg_off = 1;
-        if (c->xg_force == 1) c->xg_force = -1;
-        return prefill_chunk(c, emb, M);
     }
     c->seq_len += M;
     return 0;
@@ -1817,8 +1662,6 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
     memcpy(c->h_io, embeddings, (size_t)M * c->d * 4);
     memset(c->h_state, 0, sizeof(mdx_state));
     c->h_state->pos = c->seq_len;
-    const int xg = use_xg(c);
-    if (xg) pthread_mutex_lock(&g_persist_mu);
     int rc = mdxrt_event_record(c->ev0, c->stream);
     for (int i = 0; i < iters && !rc; i++) {
         rc = mdxrt_h2d_async(c->d_bhidden, c->h_io, (size_t)M * c->d * 4, c->stream);
@@ -1827,13 +1670,7 @@ int mdx_time_prefill(MatmulDecoderContext* c, const float* embeddings, int M, in
     }
     if (!rc) rc = mdxrt_event_record(c->ev1, c->stream);
     if (!rc) rc = mdxrt_stream_sync(c->stream);
-    const int late = !rc && xg && xg_timed_out(c);
-    if (xg) pthread_mutex_unlock(&g_persist_mu);
     if (rc) return MATMUL_DECODER_ERR_RKNN;
-    if (late) {
-        fprintf(stderr, "[BatchPrefill] a wait of the two-launch prefill timed out while timing\n");
-        return MATMUL_DECODER_ERR_RKNN;
-    }
     float ms = 0.0f;
     mdxrt_event_elapsed_ms(c->ev0, c->ev1, &ms);
     if (avg_ms) *avg_ms = ms / iters;
@@ -1901,55 +1738,6 @@ int mdx_debug_persist_kv_stream(MatmulDecoderContext* c, int mode) {
     if (!c->persist) return MATMUL_DECODER_ERR_UNSUPPORTED;
     c->kv_stream_force = mode;
     return 0;
-}
-
-int mdx_debug_prefill_xg(MatmulDecoderContext* c, int mode) {
-    if (!c || mode < -1 || mode > 1) return MATMUL_DECODER_ERR_INVALID_ARG;
-    if (!c->xg_ok) return mode == 1 ? MATMUL_DECODER_ERR_UNSUPPORTED : 0;
-    c->xg_force = mode;
-    return 0;
-}
-
-int mdx_debug_prefill_xg_spin(MatmulDecoderContext* c, unsigned rounds) {
-    if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
-    if (!c->d_xg) return MATMUL_DECODER_ERR_UNSUPPORTED;
-    if (mdxrt_fill_u32((char*)c->d_xg + 8, rounds, 1, c->stream) || mdxrt_stream_sync(c->stream))
-        return MATMUL_DECODER_ERR_RKNN;
-    return 0;
-}
-
-int mdx_trace_prefill(MatmulDecoderContext* c, const float* embeddings, int M, unsigned long long* out,
-                      size_t cap) {
-    if (!c || !embeddings || !out || M <= 0 || M > c->max_m || c->seq_len + M > c->max_seq)
-        return MATMUL_DECODER_ERR_INVALID_ARG;
-    if (!use_xg(c)) return MATMUL_DECODER_ERR_UNSUPPORTED;
-    const size_t n = (size_t)c->L * 2 * 256 * 16;
-    if (cap < n) return MATMUL_DECODER_ERR_INVALID_ARG;
-    unsigned long long* d = NULL;
-    if (mdxrt_malloc((void**)&d, n * 8)) return MATMUL_DECODER_ERR_MEMORY;
-    int rc = mdxrt_fill_u32(d, 0u, n * 2, c->stream);
-    memcpy(c->h_io, embeddings, (size_t)M * c->d * 4);
-    memset(c->h_state, 0, sizeof(mdx_state));
-    c->h_state->pos = c->seq_len;
-    pthread_mutex_lock(&g_persist_mu);
-    if (!rc) rc = mdxrt_h2d_async(c->d_bhidden, c->h_io, (size_t)M * c->d * 4, c->stream);
-    if (!rc) rc = mdxrt_h2d_async(c->d_state, c->h_state, sizeof(mdx_state), c->stream);
-    c->xg_trace = d;
-    if (!rc) rc = run_prefill_xg(c, M, c->stream);     /* eager: the graphs carry no trace */
-    c->xg_trace = NULL;
-    if (!rc) rc = mdxrt_stream_sync(c->stream);
-    const int late = !rc && xg_timed_out(c);
-    pthread_mutex_unlock(&g_persist_mu);
-    if (!rc) rc = mdxrt_d2h(out, d, n * 8);
-    mdxrt_free(d);
-    if (rc || late) return MATMUL_DECODER_ERR_RKNN;
-    c->seq_len += M;
-    return (int)(n / ((size_t)c->L * 2 * 256));
-}
-
-int mdx_prefill_path(const MatmulDecoderContext* c) {
-    if (!c) return MATMUL_DECODER_ERR_INVALID_ARG;
-    return use_xg(c) ? 1 : 0;
 }
 
 int mdx_debug_persist_local_exchange(MatmulDecoderContext* c, int mode) {

@@ -241,62 +241,6 @@ int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w
                                   const float* norm_w, float eps, uint16_t* x16_out, float* scratch,
                                   void* stream);
 
-/* hidden[M][N] += (sum of the ns split partials part[sp][64][N], in split
- * order) x scale, then x16_out = fp16((hidden * rms) * norm_w) per row
- * (norm_w NULL: no norm).  ns <= 16. */
-int mdx_launch_residual_norm(const float* part, int ns, int M, int N, const float* scale, float* hidden,
-                             const float* norm_w, float eps, uint16_t* x16_out, void* stream);
-
-/* ---- batch prefill of the 0.6B layer shape in two launches per layer
- * (mdx_prefill_xg.hip): d 1024, 16/8 heads of 128, FFN 3072, M <= 64 ---- */
-int mdx_prefill_xg_shape_ok(int d, int nq, int nkv, int hd, int F);
-/* Exchange words of the fused launches: zeroed once; word 0 is the prefill
- * counter (epochs), word 1 the status (1 after a wait timed out: the chunk's
- * results are invalid; the caller clears it and runs the chunk on the other
- * path). */
-size_t mdx_prefill_xg_buf_bytes(void);
-/* One launch of the two-launch layer: the previous launch's 8 K-split
- * partials (part_in [8][64][1024], NULL for layer 0's attention half) summed
- * in group order, x scale_in, added to the residual rows h_in [64][1024]
- * (group 0 stores the result in h_out, which must differ from h_in), the
- * RMSNorm norm_w; then the half's projections, whose 8 K-split partials go to
- * part_out (which must differ from part_in). */
-typedef struct {
-    const uint16_t* x16;           /* plain mode when not NULL: the launch's normed input
-                                      rows [M][1024] fp16 (no N stage; h_in, h_out,
-                                      part_in, scale_in and norm_w are not used) */
-    const mdx_state* state;
-    int M, n_layers, layer;
-    float eps;
-    const float* h_in;
-    float* h_out;
-    const float* part_in;
-    const float* scale_in;
-    const float* norm_w;
-    float* part_out;
-    void* xbuf;                    /* mdx_prefill_xg_buf_bytes(), zeroed once */
-    unsigned long long* trace;     /* optional: [n_layers][2][256][16] timestamps of the
-                                      100 MHz device clock, recorded by thread 0 (attention
-                                      half: 0 start, 1 loads issued, 2 N, 4 Q panel, 5 Q
-                                      MFMA, 6 Q stored, 7 R polled, 8 R, 9 A polled, 10 A
-                                      scores, 11 A, 13 O panel, 14 O MFMA, 15 end; FFN
-                                      half: 0 start, 1 loads issued, 2 N, 4 G panel, 5 G
-                                      MFMA, 6 G stored, 7 S polled, 8 S, 10 D panel, 11 D
-                                      MFMA, 12 end; others 0) */
-} mdx_prefill_xg_args;
-
-/* Attention half: q|k|v, QK-norm, RoPE at positions state->pos + t, K/V
- * appended to the layer caches, causal GQA attention, o.  qkv and o share
- * one weight kind (fp16, int8 or int4). */
-int mdx_launch_prefill_attn(const mdx_prefill_xg_args* p, const mdx_wdesc* qkv, const mdx_wdesc* o,
-                            const float* q_norm, const float* k_norm, const float* cos_t, const float* sin_t,
-                            int rope_style, uint16_t* k_cache, uint16_t* v_cache, void* stream);
-/* FFN half: gate|up, SwiGLU, down. */
-int mdx_launch_prefill_mlp(const mdx_prefill_xg_args* p, const mdx_wdesc* gu, const mdx_wdesc* down,
-                           void* stream);
-/* End of a fused prefill: state->pos += advance; the prefill counter += 1. */
-int mdx_launch_prefill_xg_end(mdx_state* state, int advance, void* xbuf, void* stream);
-
 /* QK-norm + RoPE for rows t < M at positions start+t, appending k,v fp16
  * at cache rows start+t; q written fp32 [M][nq*hd].  `start` is read from
  * state->pos. */

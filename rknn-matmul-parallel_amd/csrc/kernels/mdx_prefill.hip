@@ -991,19 +991,6 @@ int mdx_launch_gemm_residual_norm(const uint16_t* x16, int M, const mdx_wdesc* w
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int mdx_launch_residual_norm(const float* part, int ns, int M, int N, const float* scale, float* hidden,
-                             const float* norm_w, float eps, uint16_t* x16_out, void* stream) {
-    if (!part || !hidden || ns < 1 || ns > kMaxSplits || M <= 0 || M > kMaxM || N <= 0 || N % 4 ||
-        (norm_w && !x16_out))
-        return -1;
-    const int R = N % 1024 == 0 ? N / 1024 : 0;
-    auto kern = R == 1 ? k_residual_norm<1> : R == 2 ? k_residual_norm<2> : R == 4 ? k_residual_norm<4>
-                                                                                  : k_residual_norm<0>;
-    hipLaunchKernelGGL(kern, dim3(M), dim3(256), 0, (hipStream_t)stream, part, ns, N, scale, hidden, norm_w,
-                       eps, x16_out);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
 int mdx_launch_qk_rope_append_rows(const mdx_state* state, const float* qkv, int M,
                                    const float* q_norm, const float* k_norm, float eps,
                                    const float* cos_t, const float* sin_t, int nq, int nkv,

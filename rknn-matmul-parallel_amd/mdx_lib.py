@@ -125,10 +125,6 @@ def lib() -> C.CDLL:
             "mdx_last_error": (C.c_char_p, []),
             "mdx_step_token": (C.c_int, [P, C.c_int, _F]),
             "mdx_decode_path": (C.c_int, [P]),
-            "mdx_prefill_path": (C.c_int, [P]),
-            "mdx_debug_prefill_xg": (C.c_int, [P, C.c_int]),
-            "mdx_debug_prefill_xg_spin": (C.c_int, [P, C.c_uint]),
-            "mdx_trace_prefill": (C.c_int, [P, _F, C.c_int, C.POINTER(C.c_uint64), C.c_size_t]),
             "mdx_debug_persist_spin_limit": (C.c_int, [P, C.c_uint]),
             "mdx_debug_persist_kv_stream": (C.c_int, [P, C.c_int]),
             "mdx_debug_persist_local_exchange": (C.c_int, [P, C.c_int]),
@@ -370,7 +366,6 @@ class Decoder:
         self.V = c.vocab_size
         self.d = c.hidden_dim
         self.kvd = c.num_kv_heads * c.head_dim
-        self.cfg_layers = c.num_layers
         self.n_lm = c.num_lm_heads
         self.lm_vocab = c.lm_head_vocab_size if c.num_lm_heads > 1 else c.vocab_size
 
@@ -381,30 +376,6 @@ class Decoder:
         ev = lib().mdx_trace_step(self.h, token, out.ctypes.data_as(C.POINTER(C.c_uint64)), cap)
         _check(ev if ev < 0 else 0, "trace_step")
         return out[:256 * ev].reshape(256, ev)
-
-    @property
-    def prefill_path(self) -> int:
-        """1: the next prefill chunk runs in two launches per layer; 0: eight."""
-        return lib().mdx_prefill_path(self.h)
-
-    def force_prefill_path(self, mode: int) -> None:
-        """-1 default choice, 0 eight launches, 1 two launches per layer."""
-        _check(lib().mdx_debug_prefill_xg(self.h, mode), "debug_prefill_xg")
-
-    def trace_prefill(self, emb) -> np.ndarray:
-        """One two-launch prefill chunk with stage timestamps:
-        [layers][2][256][16] of the 100 MHz device clock."""
-        e = _f32(emb)
-        L = self.cfg_layers
-        out = np.zeros(L * 2 * 256 * 16, np.uint64)
-        rc = lib().mdx_trace_prefill(self.h, _p(e, _F), e.shape[0], out.ctypes.data_as(C.POINTER(C.c_uint64)),
-                                     out.size)
-        _check(rc if rc < 0 else 0, "trace_prefill")
-        return out.reshape(L, 2, 256, 16)
-
-    def force_prefill_spin(self, rounds: int) -> None:
-        """Four-launch prefill: waits give up after `rounds` polls (0: default)."""
-        _check(lib().mdx_debug_prefill_xg_spin(self.h, rounds), "debug_prefill_xg_spin")
 
     @property
     def path(self) -> int:

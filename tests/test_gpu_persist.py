@@ -318,97 +318,6 @@ def test_prefill_full_width_matches_oracle(mdx, gpu, oracle_lib, models, quant, 
     assert g.seq_len == o.seq_len == 2 * M
 
 
-def _prefill_check(oracle_lib, g, o, emb, n_rows, layers=(0, 1)):
-    """Logits of the last row and the K/V rows [0, n_rows) of a prefill chunk
-    against the oracle's (rel <= 2e-3, cosine > 0.9999, argmax or a near tie)."""
-    tok, lg = g.prefill_logits(emb)
-    assert o.prefill_batch(emb) == 0
-    x16 = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(o.last_normed())).astype(np.float64)
-    q, sc = o.lm_head_q()
-    ref = (q.astype(np.float64) @ x16) * sc
-    err = float(np.max(np.abs(lg - ref)))
-    assert rel_err(lg, ref) < 2e-3 and cosine(lg, ref) > 0.9999
-    tref = int(np.argmax(ref))
-    assert tok == tref or ref[tref] - ref[tok] <= 2 * err
-    for layer in layers:
-        kg, vg = g.kv_read(layer, 0, n_rows)
-        ko, vo = o.kv_read(layer, 0, n_rows)
-        assert rel_err(kg, ko) < 2e-3 and rel_err(vg, vo) < 2e-3, layer
-    return lg
-
-
-@pytest.mark.parametrize("quant", [0, 1, 2])
-def test_prefill_two_launches_match_oracle_and_eight_launches(mdx, gpu, oracle_lib, models, quant):
-    """The two-launch prefill (attention half and FFN half each one launch)
-    against the oracle and against the eight-launch path on the same inputs:
-    100 rows (chunks of 64 and 36, the second attending over the first), three
-    decode steps, then 33 rows starting at position 103 (cache rows before the
-    chunk read from memory, not from the exchange words).  The two paths sum
-    the K-splits differently, so they agree within the projection tolerance,
-    not bit for bit."""
-    cfg, get = models
-    path = get(quant)
-    g4, o = _pair(mdx, oracle_lib, cfg, path, quant, max_seq=512)
-    g8, _ = _pair(mdx, oracle_lib, cfg, path, quant, max_seq=512)
-    g8.force_prefill_path(0)
-    assert g4.prefill_path == 1 and g8.prefill_path == 0
-    rng = np.random.default_rng(4000 + quant)
-    e1 = rng.standard_normal((100, 1024)).astype(np.float32)
-    l4 = _prefill_check(oracle_lib, g4, o, e1, 100)
-    t8, l8 = g8.prefill_logits(e1)
-    assert rel_err(l4, l8) < 2e-3 and cosine(l4, l8) > 0.9999
-    tok = 17
-    for _ in range(3):
-        t4, _ = g4.step(tok)
-        g8.step(tok)
-        to, _ = o.step(tok)
-        tok = to
-    e2 = rng.standard_normal((33, 1024)).astype(np.float32)
-    assert g4.prefill_path == 1
-    l4 = _prefill_check(oracle_lib, g4, o, e2, 136)
-    t8, l8 = g8.prefill_logits(e2)
-    assert rel_err(l4, l8) < 2e-3 and cosine(l4, l8) > 0.9999
-    assert g4.seq_len == g8.seq_len == o.seq_len == 136
-    g4.close()
-    g8.close()
-
-
-@pytest.mark.parametrize("over", [dict(rope_style=0), dict(has_qk_norm=0)])
-def test_prefill_two_launches_rope_style_and_qk_norm(mdx, gpu, oracle_lib, models, over):
-    """Adjacent-pair RoPE (style 0, pairs (2m, 2m+1) in neighbouring lanes)
-    and a model without QK-norm through the two-launch prefill, INT8 weights,
-    60 rows then 17, against the oracle."""
-    _, get = models
-    shape = dict(SHAPE, **over)
-    cfg = mdx.qwen3_0_6b_config(name="persist-2l-var", **shape)
-    g, o = _pair(mdx, oracle_lib, cfg, get(1), 1, shape=shape, max_seq=256)
-    assert g.prefill_path == 1
-    rng = np.random.default_rng(4100 + len(str(over)))
-    _prefill_check(oracle_lib, g, o, rng.standard_normal((60, 1024)).astype(np.float32), 60)
-    _prefill_check(oracle_lib, g, o, rng.standard_normal((17, 1024)).astype(np.float32), 77)
-    g.close()
-
-
-def test_prefill_two_launch_timeout_runs_the_chunk_again(mdx, gpu, oracle_lib, models, capfd):
-    """A wait of the two-launch prefill forced to give up after one poll
-    (its kernels' own bounded wait, set from the host): the status word makes
-    the host run the chunk again on the eight-launch path, the results match
-    the oracle, and the context stays on the eight-launch path."""
-    cfg, get = models
-    g, o = _pair(mdx, oracle_lib, cfg, get(1), 1, max_seq=256)
-    assert g.prefill_path == 1
-    g.force_prefill_spin(1)
-    try:
-        rng = np.random.default_rng(4200)
-        _prefill_check(oracle_lib, g, o, rng.standard_normal((60, 1024)).astype(np.float32), 60)
-    finally:
-        g.force_prefill_spin(0)
-    assert "running the chunk again with eight launches" in capfd.readouterr().err
-    assert g.prefill_path == 0
-    _prefill_check(oracle_lib, g, o, rng.standard_normal((20, 1024)).astype(np.float32), 80)
-    g.close()
-
-
 @pytest.mark.parametrize("quant", [0, 1, 2])
 def test_prefill_panel_gemm_is_bit_identical(mdx, gpu, oracle_lib, models, quant):
     """The batch-prefill projections with the activation panel staged in LDS
@@ -424,7 +333,6 @@ def test_prefill_panel_gemm_is_bit_identical(mdx, gpu, oracle_lib, models, quant
         prev = mdx.lib().mdx_debug_gemm_rounds(rounds)
         try:
             g, _ = _pair(mdx, oracle_lib, cfg, get(quant), quant)
-            g.force_prefill_path(0)          # the eight-launch path, where these GEMMs run
             out = [g.prefill_logits(e) for e in embs]
             kv = [g.kv_read(layer, 0, 78) for layer in (0, 1)]
             g.close()
