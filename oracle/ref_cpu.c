@@ -403,35 +403,37 @@ int orc_sample_topk(float* x, int vocab_size, const int* rep, int n_rep, float p
 /* Accumulation order of the projections.  The reference runs them on the
  * NPU, whose fp32 accumulation order is not specified (src/matmul_decoder.c
  * only sees the results), so the oracle defines order 0: increasing k.
- * Order 1 accumulates k mod 4 in four separate sums combined as
- * (s0+s1)+(s2+s3): an equally valid order, used only to measure how much two
- * valid orders disagree after many layers. */
+ * Orders 1 and 2 are equally valid ones, used only to measure how much valid
+ * orders disagree after many layers: k mod 4 (order 1) or k mod 16 (order 2)
+ * in separate sums, each in increasing k, combined as a pairwise tree
+ * ((s0+s1)+(s2+s3) for four; the same levels for sixteen, the shape of a
+ * lane-parallel dot product reduced across lanes). */
 static int g_accum_order = 0;
-void orc_set_accum_order(int order) { g_accum_order = order; }
+void orc_set_accum_order(int order) { g_accum_order = order >= 0 && order <= 2 ? order : 0; }
 
-/* y[m][n] += xk * wrow[n] into the accumulator set of k (order 1: k mod 4). */
+static int accum_sets(void) { return g_accum_order == 1 ? 4 : (g_accum_order == 2 ? 16 : 1); }
+
+/* y[m][n] += xk * wrow[n] into the accumulator set of k (k mod the set count). */
 static void accum_row(float* acc, const float* wrow, float xk, int k, size_t MN_stride, int N) {
-    float* a = acc + (g_accum_order == 1 ? (size_t)(k & 3) * MN_stride : 0);
+    float* a = acc + (size_t)(k & (accum_sets() - 1)) * MN_stride;
     for (int n = 0; n < N; n++) a[n] = a[n] + xk * wrow[n];
 }
 
-static float* accum_alloc(size_t MN) {
-    return (float*)calloc((g_accum_order == 1 ? 4 : 1) * MN, sizeof(float));
-}
+static float* accum_alloc(size_t MN) { return (float*)calloc((size_t)accum_sets() * MN, sizeof(float)); }
 
-static void accum_finish(float* y, const float* acc, size_t MN) {
-    if (g_accum_order == 1) {
-        for (size_t i = 0; i < MN; i++) y[i] = (acc[i] + acc[MN + i]) + (acc[2 * MN + i] + acc[3 * MN + i]);
-    } else {
-        memcpy(y, acc, MN * sizeof(float));
-    }
+/* The sets combined pairwise: (s0+s1), (s2+s3), ... then the pairs of those. */
+static void accum_finish(float* y, float* acc, size_t MN) {
+    for (int w = accum_sets(); w > 1; w /= 2)
+        for (int j = 0; j < w / 2; j++)
+            for (size_t i = 0; i < MN; i++) acc[(size_t)j * MN + i] = acc[(size_t)(2 * j) * MN + i] + acc[(size_t)(2 * j + 1) * MN + i];
+    memcpy(y, acc, MN * sizeof(float));
 }
 
 /* Reference: src/matmul_decoder.c:382-445 (type 1) and :1841-1899 (batch).
  * fp32 input rounded to fp16, products exact in fp32, fp32 accumulation in
  * increasing k. */
 void orc_matmul_f16(float* y, const float* x, const uint16_t* w, int M, int K, int N) {
-    if (g_accum_order == 1) {
+    if (g_accum_order != 0) {
         const size_t MN = (size_t)M * N;
         float* acc = accum_alloc(MN);
         float* wrow = (float*)malloc(sizeof(float) * (size_t)N);

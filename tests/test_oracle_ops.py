@@ -280,14 +280,24 @@ def test_matmul_accumulation_orders(oracle_lib):
     exact = (xi.astype(np.int64) @ q.astype(np.int64)).astype(np.float32)
     ys = {}
     try:
-        for order in (0, 1):
+        for order in (0, 1, 2):
             oracle_lib.lib().orc_set_accum_order(order)
             ys[order] = oracle_lib.matmul(0, x, w.view(np.uint16), None, M, K, N)
             assert rel_err(ys[order], want) < 1e-5
             assert np.array_equal(oracle_lib.matmul(1, xi, q, None, M, K, N), exact)
     finally:
         oracle_lib.lib().orc_set_accum_order(0)
-    assert not np.array_equal(ys[0], ys[1])
+    assert not np.array_equal(ys[0], ys[1]) and not np.array_equal(ys[0], ys[2])
+    assert not np.array_equal(ys[1], ys[2])
+    # order 2 by hand: 16 sums of k mod 16 in increasing k, then a pairwise tree
+    x16 = x.astype(np.float16).astype(np.float32)
+    wf = w.astype(np.float32)
+    sums = np.zeros((16, M, N), np.float32)
+    for k in range(K):
+        sums[k % 16] = sums[k % 16] + np.outer(x16[:, k], wf[k]).astype(np.float32)
+    while len(sums) > 1:
+        sums = np.stack([sums[2 * j] + sums[2 * j + 1] for j in range(len(sums) // 2)])
+    assert np.array_equal(sums[0], ys[2])
     assert np.array_equal(oracle_lib.matmul(0, x, w.view(np.uint16), None, M, K, N), ys[0])
 
 
