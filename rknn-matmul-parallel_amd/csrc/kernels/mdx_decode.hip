@@ -106,54 +106,106 @@ __device__ __forceinline__ float chunk_dot(uint4 w, const uint4* xs, int j, floa
     }
 }
 
+// x is read as 4-element vectors (K is a multiple of 4 for every kind),
+// kXV per thread at a time, all loads of a batch issued before the first is
+// used (indexes clamped to the last vector, so no load needs a branch):
+// staging costs one cache round trip per batch, where a load-use loop would
+// wait on each element for every earlier load, the weights included.
+constexpr int kXV = 2;
+
 // Builds the activation vector in LDS: fp16 for the NPU-style kinds, fp32 for
 // the CPU-GEMV kinds.  XM_NORM / XM_EMBED apply the reference RMSNorm first.
 template <bool XF32>
 __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* red) {
-    const int tid = threadIdx.x;
-    const int K = a.K;
-    const float* src = a.xf32;
-    if (a.xmode == XM_EMBED) {
-        if (a.st_in->mode != 1) {
-            int tok = a.st_in->token;
-            tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
-            src = a.emb_table + (size_t)tok * K;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int K = a.K, nv = K / 4, step = kXV * nt;
+    float4* xs32 = reinterpret_cast<float4*>(xs_raw);
+    uint2* xs16 = reinterpret_cast<uint2*>(xs_raw);
+    if (a.xmode == XM_F16) {
+        const uint2* x16 = reinterpret_cast<const uint2*>(a.x16);
+        for (int q0 = tid; q0 < nv; q0 += step) {
+            uint2 h[kXV];
+#pragma unroll
+            for (int i = 0; i < kXV; i++) h[i] = x16[min(q0 + i * nt, nv - 1)];
+#pragma unroll
+            for (int i = 0; i < kXV; i++) {
+                const int q = q0 + i * nt;
+                if (q >= nv) break;
+                if constexpr (XF32)
+                    xs32[q] = make_float4(f16_bits_to_f32(h[i].x & 0xffff), f16_bits_to_f32(h[i].x >> 16),
+                                          f16_bits_to_f32(h[i].y & 0xffff), f16_bits_to_f32(h[i].y >> 16));
+                else xs16[q] = h[i];
+            }
         }
-        if (blockIdx.x == 0)
-            for (int k = tid; k < K; k += blockDim.x) a.hidden_out[k] = src[k];
+        __syncthreads();
+        return;
     }
-    const bool norm = a.xmode == XM_NORM || a.xmode == XM_EMBED;
+    const float* src = a.xf32;
+    const bool embed = a.xmode == XM_EMBED;
+    if (embed && a.st_in->mode != 1) {
+        int tok = a.st_in->token;
+        tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
+        src = a.emb_table + (size_t)tok * K;
+    }
+    const bool norm = a.xmode == XM_NORM || embed;
+    const bool copy = embed && blockIdx.x == 0;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    const float4* g4 = reinterpret_cast<const float4*>(a.norm_w);
+    float4 v[kXV], g[kXV];
+#pragma unroll
+    for (int i = 0; i < kXV; i++) v[i] = s4[min(tid + i * nt, nv - 1)];
+    if (norm) {
+#pragma unroll
+        for (int i = 0; i < kXV; i++) g[i] = g4[min(tid + i * nt, nv - 1)];
+    }
     float rms = 1.0f;
     if (norm) {
         float ss = 0.0f;
-        for (int k = tid; k < K; k += blockDim.x) {
-            const float v = src[k];
-            ss += v * v;
+        for (int q0 = tid; q0 < nv; q0 += step) {
+            float4 u[kXV];
+#pragma unroll
+            for (int i = 0; i < kXV; i++) u[i] = q0 == tid ? v[i] : s4[min(q0 + i * nt, nv - 1)];
+#pragma unroll
+            for (int i = 0; i < kXV; i++) {
+                const int q = q0 + i * nt;
+                if (q >= nv) break;
+                if (copy) reinterpret_cast<float4*>(a.hidden_out)[q] = u[i];
+                ss += u[i].x * u[i].x;
+                ss += u[i].y * u[i].y;
+                ss += u[i].z * u[i].z;
+                ss += u[i].w * u[i].w;
+            }
         }
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         float tot = 0.0f;
-        for (int wv = 0; wv < (int)(blockDim.x >> 6); wv++) tot += red[wv];
+        for (int wv = 0; wv < (nt >> 6); wv++) tot += red[wv];
         rms = 1.0f / sqrtf(tot / (float)K + a.eps);
     }
-    if constexpr (XF32) {
-        float* xs = reinterpret_cast<float*>(xs_raw);
-        for (int k = tid; k < K; k += blockDim.x) {
-            float v;
-            if (norm) v = (src[k] * rms) * a.norm_w[k];
-            else if (a.xmode == XM_F16) v = f16_bits_to_f32(a.x16[k]);
-            else v = src[k];
-            xs[k] = v;
+    for (int q0 = tid; q0 < nv; q0 += step) {
+        if (q0 != tid) {
+#pragma unroll
+            for (int i = 0; i < kXV; i++) {
+                const int q = min(q0 + i * nt, nv - 1);
+                v[i] = s4[q];
+                if (norm) g[i] = g4[q];
+            }
         }
-    } else {
-        uint16_t* xs = reinterpret_cast<uint16_t*>(xs_raw);
-        for (int k = tid; k < K; k += blockDim.x) {
-            uint16_t v;
-            if (norm) v = f32_to_f16_bits((src[k] * rms) * a.norm_w[k]);
-            else if (a.xmode == XM_F16) v = a.x16[k];
-            else v = f32_to_f16_bits(src[k]);
-            xs[k] = v;
+#pragma unroll
+        for (int i = 0; i < kXV; i++) {
+            const int q = q0 + i * nt;
+            if (q >= nv) break;
+            float4 x = v[i];
+            if (norm) {
+                x.x = (x.x * rms) * g[i].x;
+                x.y = (x.y * rms) * g[i].y;
+                x.z = (x.z * rms) * g[i].z;
+                x.w = (x.w * rms) * g[i].w;
+            }
+            if constexpr (XF32) xs32[q] = x;
+            else xs16[q] = make_uint2((uint32_t)f32_to_f16_bits(x.x) | ((uint32_t)f32_to_f16_bits(x.y) << 16),
+                                      (uint32_t)f32_to_f16_bits(x.z) | ((uint32_t)f32_to_f16_bits(x.w) << 16));
         }
     }
     __syncthreads();
@@ -169,7 +221,8 @@ struct RowSet {
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             const int slot = slot0 + r;
-            const int unit = slot / a.unit_rows, which = slot % a.unit_rows;
+            // unit_rows is 1 or 2
+            const int unit = slot >> (a.unit_rows - 1), which = slot & (a.unit_rows - 1);
             valid[r] = unit < a.n_units;
             rows[r] = unit + which * a.n_units;
             sc[r] = (a.scale && valid[r]) ? a.scale[rows[r]] : 1.0f;
@@ -188,6 +241,34 @@ struct RowSet {
         }
     }
 };
+
+// The stores of a wave's RW reduced rows (lane r stores row r).
+template <int KIND, int RW, int U>
+__device__ __forceinline__ void store_rows(const GemvArgs& a, const RowSet<KIND, RW, U>& cur,
+                                           const float (&y)[RW], int lane) {
+    if (a.epi == EP_SWIGLU) {
+        // slots come in (gate, up) pairs: slot 2c is row unit, 2c+1 row unit + F
+#pragma unroll
+        for (int r = 0; r + 1 < RW; r += 2) {
+            if (cur.valid[r] && lane == r) {
+                const int unit = cur.rows[r];
+                const float g = y[r], u = y[r + 1];
+                float v;
+                if (unit < (a.n_units & ~3)) v = silu_mul(g, u);
+                else v = (g / (1.0f + expf(-g))) * u;     // reference tail formula
+                a.out_f16[unit] = f32_to_f16_bits(v);
+            }
+        }
+    } else {     // EP_STORE, EP_ADD, and the logits of EP_LOGITS
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            if (cur.valid[r] && lane == r) {
+                if (a.epi == EP_ADD) a.out_f32[cur.rows[r]] = a.out_f32[cur.rows[r]] + y[r];
+                else a.out_f32[cur.rows[r]] = y[r];
+            }
+        }
+    }
+}
 
 // The GEMV.  Blocks of 256 threads (4 waves x RW rows) walk the row blocks
 // with a grid stride; the next row block's weights are requested before the
@@ -245,28 +326,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             y[r] = wave_sum_dpp(acc[r]);
             if (a.scale && cur.valid[r]) y[r] = y[r] * cur.sc[r];
         }
-        if (a.epi == EP_SWIGLU) {
-            // slots come in (gate, up) pairs: slot 2c is row unit, 2c+1 row unit + F
-#pragma unroll
-            for (int r = 0; r + 1 < RW; r += 2) {
-                if (cur.valid[r] && lane == r) {
-                    const int unit = cur.rows[r];
-                    const float g = y[r], u = y[r + 1];
-                    float v;
-                    if (unit < (a.n_units & ~3)) v = silu_mul(g, u);
-                    else v = (g / (1.0f + expf(-g))) * u;     // reference tail formula
-                    a.out_f16[unit] = f32_to_f16_bits(v);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < RW; r++) {
-                if (cur.valid[r] && lane == r) {
-                    if (a.epi == EP_ADD) a.out_f32[cur.rows[r]] = a.out_f32[cur.rows[r]] + y[r];
-                    else a.out_f32[cur.rows[r]] = y[r];
-                }
-            }
-        }
+        store_rows<KIND, RW, U>(a, cur, y, lane);
         if (a.epi == EP_LOGITS) {
 #pragma unroll
             for (int r = 0; r < RW; r++) {
@@ -308,6 +368,41 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             st->pos = st->pos + a.advance;
         }
     }
+}
+
+// The GEMV when every workgroup takes exactly one row block and a lane's
+// loads cover the whole row in one round (K <= 64 * U * E): the same weight
+// requests, staging and sums as k_gemv, in a straight-line kernel without
+// the grid-stride loop and the argmax tail.  A launch this small is bound by
+// its fixed costs (dispatch and one HBM round trip), and the shorter code
+// leaves fewer instruction-cache lines to fetch after the launch.
+template <int KIND, int RW, int U>
+__global__ __launch_bounds__(256) void k_gemv_once(GemvArgs a) {
+    using T = KindTraits<KIND>;
+    extern __shared__ uint4 xs[];
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int nchunks = a.K / T::E;
+    const size_t row_bytes = (size_t)a.K * T::EB2 / 2;
+    RowSet<KIND, RW, U> rs;
+    uint4 wv[RW][U];
+    rs.init(a, blockIdx.x, wave);
+    rs.load(a, row_bytes, nchunks, 0, lane, wv);
+    build_x<T::XF32>(a, xs, red);
+    float y[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = u * 64 + lane;
+            if (j < nchunks) acc = chunk_dot<KIND>(wv[r][u], xs, j, acc);
+        }
+        y[r] = wave_sum_dpp(acc);
+        if (a.scale && rs.valid[r]) y[r] = y[r] * rs.sc[r];
+    }
+    store_rows<KIND, RW, U>(a, rs, y, lane);
 }
 
 // INT8 lm_head with K = 1024 (one 16-byte chunk per lane is a whole row):
@@ -455,6 +550,36 @@ GemvKernel pick_kernel(int rw, int u) {
 #undef MDX_U_CASES
 }
 
+template <int KIND>
+GemvKernel pick_once_kernel(int rw, int u) {
+#define MDX_U_CASES(RW_)                                  \
+    switch (u) {                                          \
+        case 1: return k_gemv_once<KIND, RW_, 1>;         \
+        case 2: return k_gemv_once<KIND, RW_, 2>;         \
+        case 3: return k_gemv_once<KIND, RW_, 3>;         \
+        case 4: return k_gemv_once<KIND, RW_, 4>;         \
+        case 6: return k_gemv_once<KIND, RW_, 6>;         \
+        default: return k_gemv_once<KIND, RW_, 8>;        \
+    }
+    switch (rw) {
+        case 1: MDX_U_CASES(1)
+        case 2: MDX_U_CASES(2)
+        case 4: MDX_U_CASES(4)
+        default: MDX_U_CASES(8)
+    }
+#undef MDX_U_CASES
+}
+
+GemvKernel pick_once(int kind, int rw, int u) {
+    switch (kind) {
+        case KF16: return pick_once_kernel<KF16>(rw, u);
+        case KI8: return pick_once_kernel<KI8>(rw, u);
+        case KI4: return pick_once_kernel<KI4>(rw, u);
+        case KF32X: return pick_once_kernel<KF32X>(rw, u);
+        default: return pick_once_kernel<KF16X>(rw, u);
+    }
+}
+
 GemvKernel pick(int kind, int rw, int u) {
     switch (kind) {
         case KF16: return pick_kernel<KF16>(rw, u);
@@ -509,7 +634,11 @@ int launch_gemv(int kind, GemvArgs a, int rw, int max_grid, void* stream) {
     const bool xf32 = kind == KF32X || kind == KF16X;
     const size_t lds = (size_t)a.K * (xf32 ? 4 : 2);
     if (lds > 64 * 1024) return -5;
-    GemvKernel k = pick(kind, rw, u);
+    // one row block per workgroup and one round of loads per row: the
+    // straight-line kernel
+    const long nblk = (slots + 4L * rw - 1) / (4L * rw);
+    const bool once = a.epi != EP_LOGITS && grid == nblk && nchunks <= 64 * u;
+    GemvKernel k = once ? pick_once(kind, rw, u) : pick(kind, rw, u);
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
