@@ -149,6 +149,30 @@ def run_sampling(mdx, cfg, max_seq: int, args) -> int:
     return 0
 
 
+def layer_stage_split(traces, n_layers: int) -> dict:
+    """Stage times (us) of one layer inside the one-launch step, from traced
+    steps ([workgroups][events] of 100 MHz device timestamps, 16 events per
+    layer): the four projection stages (input staged -> result published),
+    the exchange waits before them, and the whole layer.  Medians over the 256
+    workgroups, means over layers 2 .. L-3 and over the traced steps."""
+    seg = {"qkv": (1, 2), "o": (6, 7), "gate_up": (8, 9), "down": (10, 11),
+           "wait_h_before_qkv": (11, 17), "wait_attn_before_o": (5, 6),
+           "wait_h_before_gate_up": (7, 8), "wait_act_before_down": (9, 10), "layer": (0, 16)}
+    acc = {k: [] for k in seg}
+    for tr in traces:
+        x = np.asarray(tr, np.int64) * 0.01
+        for lay in range(2, n_layers - 2):
+            base = 16 * lay
+            for k, (a, b) in seg.items():
+                acc[k].append(float(np.median(x[:, base + b] - x[:, base + a])))
+    out = {k: round(float(np.mean(v)), 3) for k, v in acc.items()}
+    out["projections_sum"] = round(out["qkv"] + out["o"] + out["gate_up"] + out["down"], 3)
+    out["source"] = ("mdx_trace_step: medians over 256 workgroups, mean over layers 2..25 of 3 "
+                     "traced steps; wait_h_before_qkv spans the previous layer's last event to "
+                     "this layer's staged input")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -177,9 +201,10 @@ def main() -> int:
         args.no_prefill = args.no_cpu_baseline = True
     kv0 = 4096 if w4 else KV_PREFILL
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build runs the decoder on a single MI355X and has "
-              "no multi-GPU path (see DESIGN.md for how it would shard); use --gpus 1.",
-              file=sys.stderr)
+        print("bench.py measures one GPU: the decoder runs on a single MI355X and there is no "
+              "multi-GPU path (the weights, 881 MB, fit one GPU's HBM many times over: independent "
+              "sequences would each run on their own GPU with replicated weights, and a tensor-"
+              "parallel split would cost two small all-reduces per layer); use --gpus 1.", file=sys.stderr)
         return 2
 
     import mdx_lib as mdx
@@ -264,6 +289,14 @@ def main() -> int:
     if not args.probe and not w4:
         dec.time_projection("layer", 28)
         layer_us, layer_bytes = dec.time_projection("layer", 280)
+    # the same projections inside the one-launch step (the path the decode
+    # figure runs): stage times from traced steps
+    one_launch_stages = None
+    if not args.probe and not w4 and dec.path == 1:
+        dec.kv_fill_normal(kv0, 1003)
+        dec.trace_step(START_TOKEN)
+        one_launch_stages = layer_stage_split([dec.trace_step(START_TOKEN) for _ in range(3)],
+                                              d["num_layers"])
     path_kind = dec.path
     dec.close()
     step_us = dev_ms * 1000.0 / args.steps
@@ -281,7 +314,8 @@ def main() -> int:
             "avg_us": round(us, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
             "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
             "kernels": "k_gemv: RMSNorm+q|k|v, o+residual, RMSNorm+gate|up+SwiGLU, down+residual",
-            "rotation": "28 layers' distinct weights (881 MB), launches replayed from a captured graph"}
+            "rotation": "28 layers' distinct weights (881 MB), launches replayed from a captured graph",
+            "one_launch_stages": one_launch_stages}
         log(f"config 2 layer projections: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
         # ---- config 1: the INT8 lm_head tile GEMV 1 x 1024 x 4096 ----
         us1 = mdx.time_gemv(1, 1024, 4096, 128, 1024)
