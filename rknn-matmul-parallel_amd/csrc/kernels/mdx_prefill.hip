@@ -572,11 +572,38 @@ __global__ __launch_bounds__(64) void k_qk_rope_append_rows(
     __shared__ float rowv[2 * 64 * kRopePairs];
     const float* slice;
     if (part) {
-        // the qkv GEMM's K-split partials, summed in split order, times the column scale
-        for (int e = lane; e < hd; e += 64) {
-            float v = part[(size_t)t * nn + c0 + e];
-            for (int sp = 1; sp < ns; sp++) v = v + part[((size_t)sp * kMaxM + t) * nn + c0 + e];
-            rowv[e] = pscale ? v * pscale[c0 + e] : v;
+        // the qkv GEMM's K-split partials, summed in split order, times the
+        // column scale.  Lane elements e = lane + 64k (k < kRopeE, hd <= 256);
+        // every load of a batch of kRopeS splits is issued before any is used
+        // (indexes clamped to the slice's last column), so the block waits for
+        // memory once per batch instead of once per split and element.
+        constexpr int kRopeE = 4, kRopeS = 4;
+        float acc[kRopeE], ps[kRopeE];
+#pragma unroll
+        for (int k = 0; k < kRopeE; k++) {
+            const int e = min(lane + 64 * k, hd - 1);
+            acc[k] = part[(size_t)t * nn + c0 + e];
+            ps[k] = pscale ? pscale[c0 + e] : 1.0f;
+        }
+        for (int sp0 = 1; sp0 < ns; sp0 += kRopeS) {
+            float p[kRopeS][kRopeE];
+#pragma unroll
+            for (int s = 0; s < kRopeS; s++)
+#pragma unroll
+                for (int k = 0; k < kRopeE; k++) {
+                    const int sp = min(sp0 + s, ns - 1), e = min(lane + 64 * k, hd - 1);
+                    p[s][k] = part[((size_t)sp * kMaxM + t) * nn + c0 + e];
+                }
+#pragma unroll
+            for (int s = 0; s < kRopeS; s++)
+                if (sp0 + s < ns)
+#pragma unroll
+                    for (int k = 0; k < kRopeE; k++) acc[k] = acc[k] + p[s][k];
+        }
+#pragma unroll
+        for (int k = 0; k < kRopeE; k++) {
+            const int e = lane + 64 * k;
+            if (e < hd) rowv[e] = pscale ? acc[k] * ps[k] : acc[k];
         }
         __syncthreads();
         slice = rowv;
