@@ -530,63 +530,48 @@ __global__ __launch_bounds__(256) void k_lmhead_i8_1k(GemvArgs a) {
 
 typedef void (*GemvKernel)(GemvArgs);
 
-template <int KIND>
+// The instantiated shapes: RW = 1 or 2 rows per wave with U = 1, 2, 3, 4, 6
+// or 8 chunks per lane, and RW = 8 with U = 1 or 2 (RW * U <= 16, the
+// choices of rows_per_wave_for and pick_u).  ONCE selects k_gemv_once.
+template <int KIND, bool ONCE, int RW, int U>
+constexpr GemvKernel gemv_fn() {
+    if constexpr (ONCE) return k_gemv_once<KIND, RW, U>;
+    else return k_gemv<KIND, RW, U>;
+}
+
+template <int KIND, bool ONCE, int RW>
+GemvKernel pick_u_kernel(int u) {
+    if constexpr (RW == 8) {
+        return u == 1 ? gemv_fn<KIND, ONCE, 8, 1>() : gemv_fn<KIND, ONCE, 8, 2>();
+    } else {
+        switch (u) {
+            case 1: return gemv_fn<KIND, ONCE, RW, 1>();
+            case 2: return gemv_fn<KIND, ONCE, RW, 2>();
+            case 3: return gemv_fn<KIND, ONCE, RW, 3>();
+            case 4: return gemv_fn<KIND, ONCE, RW, 4>();
+            case 6: return gemv_fn<KIND, ONCE, RW, 6>();
+            default: return gemv_fn<KIND, ONCE, RW, 8>();
+        }
+    }
+}
+
+template <int KIND, bool ONCE>
 GemvKernel pick_kernel(int rw, int u) {
-#define MDX_U_CASES(RW_)                               \
-    switch (u) {                                       \
-        case 1: return k_gemv<KIND, RW_, 1>;           \
-        case 2: return k_gemv<KIND, RW_, 2>;           \
-        case 3: return k_gemv<KIND, RW_, 3>;           \
-        case 4: return k_gemv<KIND, RW_, 4>;           \
-        case 6: return k_gemv<KIND, RW_, 6>;           \
-        default: return k_gemv<KIND, RW_, 8>;          \
-    }
     switch (rw) {
-        case 1: MDX_U_CASES(1)
-        case 2: MDX_U_CASES(2)
-        case 4: MDX_U_CASES(4)
-        default: MDX_U_CASES(8)
+        case 1: return pick_u_kernel<KIND, ONCE, 1>(u);
+        case 2: return pick_u_kernel<KIND, ONCE, 2>(u);
+        default: return pick_u_kernel<KIND, ONCE, 8>(u);
     }
-#undef MDX_U_CASES
 }
 
-template <int KIND>
-GemvKernel pick_once_kernel(int rw, int u) {
-#define MDX_U_CASES(RW_)                                  \
-    switch (u) {                                          \
-        case 1: return k_gemv_once<KIND, RW_, 1>;         \
-        case 2: return k_gemv_once<KIND, RW_, 2>;         \
-        case 3: return k_gemv_once<KIND, RW_, 3>;         \
-        case 4: return k_gemv_once<KIND, RW_, 4>;         \
-        case 6: return k_gemv_once<KIND, RW_, 6>;         \
-        default: return k_gemv_once<KIND, RW_, 8>;        \
-    }
-    switch (rw) {
-        case 1: MDX_U_CASES(1)
-        case 2: MDX_U_CASES(2)
-        case 4: MDX_U_CASES(4)
-        default: MDX_U_CASES(8)
-    }
-#undef MDX_U_CASES
-}
-
-GemvKernel pick_once(int kind, int rw, int u) {
+template <bool ONCE>
+GemvKernel pick_kind(int kind, int rw, int u) {
     switch (kind) {
-        case KF16: return pick_once_kernel<KF16>(rw, u);
-        case KI8: return pick_once_kernel<KI8>(rw, u);
-        case KI4: return pick_once_kernel<KI4>(rw, u);
-        case KF32X: return pick_once_kernel<KF32X>(rw, u);
-        default: return pick_once_kernel<KF16X>(rw, u);
-    }
-}
-
-GemvKernel pick(int kind, int rw, int u) {
-    switch (kind) {
-        case KF16: return pick_kernel<KF16>(rw, u);
-        case KI8: return pick_kernel<KI8>(rw, u);
-        case KI4: return pick_kernel<KI4>(rw, u);
-        case KF32X: return pick_kernel<KF32X>(rw, u);
-        default: return pick_kernel<KF16X>(rw, u);
+        case KF16: return pick_kernel<KF16, ONCE>(rw, u);
+        case KI8: return pick_kernel<KI8, ONCE>(rw, u);
+        case KI4: return pick_kernel<KI4, ONCE>(rw, u);
+        case KF32X: return pick_kernel<KF32X, ONCE>(rw, u);
+        default: return pick_kernel<KF16X, ONCE>(rw, u);
     }
 }
 
@@ -626,6 +611,7 @@ int rows_per_wave_for(int rows) {
 int launch_gemv(int kind, GemvArgs a, int rw, int max_grid, void* stream) {
     const int E = elems_per_chunk(kind);
     if (a.K <= 0 || a.K % E != 0 || a.n_units <= 0) return -1;
+    if (rw != 1 && rw != 2 && rw != 8) return -1;   // the instantiated row counts
     const int nchunks = a.K / E;
     const int u = pick_u(nchunks, rw);
     const long slots = (long)a.n_units * a.unit_rows;
@@ -638,7 +624,7 @@ int launch_gemv(int kind, GemvArgs a, int rw, int max_grid, void* stream) {
     // straight-line kernel
     const long nblk = (slots + 4L * rw - 1) / (4L * rw);
     const bool once = a.epi != EP_LOGITS && grid == nblk && nchunks <= 64 * u;
-    GemvKernel k = once ? pick_once(kind, rw, u) : pick(kind, rw, u);
+    GemvKernel k = once ? pick_kind<true>(kind, rw, u) : pick_kind<false>(kind, rw, u);
     hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
