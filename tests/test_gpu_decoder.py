@@ -306,7 +306,9 @@ def test_pybind_module_end_to_end(mdx, gpu, oracle_lib, models):
 
 @pytest.mark.parametrize("M,K", [(1, 1024), (5, 1024), (64, 1024), (70, 1024),
                                  # any K, as the reference accepts (zero-padded to 32)
-                                 (1, 100), (3, 1000), (67, 33), (1, 7)])
+                                 (1, 100), (3, 1000), (67, 33), (1, 7),
+                                 # M=1 activations staged in two and three batches
+                                 (1, 3072), (1, 4128)])
 def test_rmp_run_matches_oracle(mdx, gpu, oracle_lib, M, K):
     L = mdx.lib()
     N = 1024

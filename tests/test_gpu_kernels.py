@@ -307,6 +307,35 @@ def test_lm_head_argmax_signed_zero_and_nan(mdx, gpu, oracle_lib, K, V):
     assert tok == oracle_lib.argmax(lg) == 700
 
 
+@pytest.mark.parametrize("K", [2080, 3072, 4096])
+@pytest.mark.parametrize("kind", [1, 3, 4])
+def test_lm_head_wide_rows_norm_staging(mdx, gpu, oracle_lib, kind, K):
+    """Hidden sizes above one staging batch of the GEMV (2048 values for 256
+    threads): the RMSNorm's sum of squares and the staged activations span
+    two batches, the second one partial at K = 2080.  INT8 rows multiply the
+    fp16-rounded normed activations, fp32 and fp16 rows the fp32 ones."""
+    rng = np.random.default_rng(K + 17 * kind)
+    V = 640
+    h = rng.standard_normal(K).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    x = oracle_lib.rms_norm(h, nw, 1e-6)
+    w = (rng.standard_normal((V, K)) * 0.02).astype(np.float32)
+    if kind == 1:
+        q, s = oracle_lib.quantize_lm_head(oracle_lib.f32_to_f16(w), V, K)
+        tok, lg = mdx.lmhead(1, K, V, q, s, h, nw, 1e-6)
+        x16 = oracle_lib.f16_to_f32(oracle_lib.f32_to_f16(x))
+        ref = (q.astype(np.float64) @ x16.astype(np.float64)) * s
+        assert rel_err(lg, ref) < TOL * 0.1 and cosine(lg, ref) > 0.9999
+    elif kind == 3:
+        tok, lg = mdx.lmhead(3, K, V, w, None, h, nw, 1e-6)
+        assert rel_err(lg, oracle_lib.gemv_rows_f32(x, w, V, K)) < 1e-5
+    else:
+        w16 = _f16_bits(w)
+        tok, lg = mdx.lmhead(4, K, V, w16, None, h, nw, 1e-6)
+        assert rel_err(lg, oracle_lib.gemv_rows_f16(x, w16, V, K)) < 1e-5
+    assert tok == int(np.argmax(lg))
+
+
 def test_lm_head_fp32_and_fp16_rows(mdx, gpu, oracle_lib):
     rng = np.random.default_rng(11)
     K, V = 1024, 2048
