@@ -149,6 +149,17 @@ def run_sampling(mdx, cfg, max_seq: int, args) -> int:
     return 0
 
 
+def profile_traffic(name: str) -> dict | None:
+    """HBM traffic of a kernel or launch sequence from the committed rocprofv3
+    counter summary profiles/<name>_traffic.json (FETCH_SIZE and WRITE_SIZE
+    passes scaled by a copy kernel's counts), or None."""
+    path = os.path.join(ROOT, "profiles", name + "_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
 def layer_stage_split(traces, n_layers: int) -> dict:
     """Stage times (us) of one layer inside the one-launch step, from traced
     steps ([workgroups][events] of 100 MHz device timestamps, 16 events per
@@ -301,10 +312,9 @@ def main() -> int:
     dec.close()
     step_us = dev_ms * 1000.0 / args.steps
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "k_persist_step_fp16_decode_kv512_traffic.json")
-    if os.path.exists(tfile) and not w4:
-        with open(tfile) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    tdoc = None if w4 else profile_traffic("k_persist_step_fp16_decode_kv512")
+    if tdoc:
+        traffic = tdoc.get("hbm_bytes_per_launch")
 
     configs = {}
     if not args.probe and not w4:
@@ -353,9 +363,15 @@ def main() -> int:
                             + 4.0 * (4096 + 1024 + 6144 + 1024) + 4.0 * (2 * 1024 + 256))
         flops = 2.0 * 60 * 28 * (1024 * 4096 + 2048 * 1024 + 2 * 1024 * 3072 + 3072 * 1024)
         dec8.close()
+        ptr = profile_traffic("k_gemm_prefill_m60_int8")
         prefill = {"ms": round(pms, 4), "tokens": 60,
                    "hbm_frac_layers": round(layer_bytes / (pms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                    "mfma_frac_layers": round(flops / (pms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4),
+                   "algorithmic_bytes": layer_bytes,
+                   "traffic": ptr["hbm_bytes_per_prefill"] if ptr else None,
+                   "traffic_source": ("profiles/k_gemm_prefill_m60_int8_traffic.json: rocprofv3 FETCH_SIZE "
+                                      "and WRITE_SIZE passes over the same prefill, scaled by a copy "
+                                      "kernel's counts (not this run)") if ptr else None,
                    "note": "28 INT8 layers, causal GQA over 60 positions, device time (HIP events)"}
         log(f"prefill M=60: {pms:.3f} ms")
 
@@ -377,6 +393,7 @@ def main() -> int:
         wall5 = time.perf_counter() - t0
         dec4.close()
         b5 = step_bytes(d5, list(range(4096, 4096 + n5)), 2)
+        tr5 = profile_traffic("k_persist_step_int4_decode_kv4096")
         us5 = dev5 * 1000.0 / n5
         configs["5_w4a16_decode_kv4096"] = {
             "ms_per_token": round(wall5 * 1000.0 / n5, 5), "tokens_per_s": round(n5 / wall5, 2),
@@ -384,7 +401,12 @@ def main() -> int:
             "roofline": {"bound": "hbm", "kernel": "k_persist_step<i4>", "avg_us": round(us5, 2),
                          "bytes_per_launch": b5, "achieved": round(b5 / (us5 * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(b5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                         "frac": round(b5 / (us5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": tr5["hbm_bytes_per_launch"] if tr5 else None,
+                         "traffic_source": ("profiles/k_persist_step_int4_decode_kv4096_traffic.json: "
+                                            "rocprofv3 FETCH_SIZE and WRITE_SIZE passes over the same "
+                                            "kernel at KV 4096..4105, scaled by a copy kernel's counts "
+                                            "(not this run)") if tr5 else None},
             "tokens_head": toks5[:8]}
         log(f"config 5 W4A16 KV 4096: {wall5 * 1000.0 / n5 * 1000:.1f} us/token wall, {us5:.1f} us device")
 
