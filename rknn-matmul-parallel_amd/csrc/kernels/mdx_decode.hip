@@ -680,28 +680,51 @@ __device__ __forceinline__ void attn_plan(int L, int max_splits, int& splits, in
 // Per-head RMSNorm (optional) + RoPE of one head vector, one wave.  Writes the
 // rotated fp32 values to dst (LDS) and, when cache != NULL, their fp16
 // roundings to cache (and the rounded values to dst, the fp16 KV semantic).
+// hd <= 256: a lane holds elements lane + 64k (k < 4) for the sum of squares
+// (summed in that order) and pairs i = lane + 64k (k < 2); every load is
+// issued before the first is used (indexes clamped into the head).
 __device__ __forceinline__ void rope_head(const float* src, const float* nw, float eps,
                                           const float* cr, const float* sr, int hd, int style,
                                           float* dst, uint16_t* cache, int lane) {
     const int half = hd / 2;
+    float xe[4], x0[2], x1[2], w0[2], w1[2], cv[2], sv[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) xe[k] = src[min(lane + 64 * k, hd - 1)];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = min(lane + 64 * k, half - 1);
+        const int i0 = style == 0 ? 2 * i : i;
+        const int i1 = style == 0 ? 2 * i + 1 : i + half;
+        x0[k] = src[i0];
+        x1[k] = src[i1];
+        w0[k] = nw ? nw[i0] : 1.0f;
+        w1[k] = nw ? nw[i1] : 1.0f;
+        cv[k] = cr[i];
+        sv[k] = sr[i];
+    }
     float rms = 1.0f;
     if (nw) {
         float ss = 0.0f;
-        for (int e = lane; e < hd; e += 64) ss += src[e] * src[e];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (lane + 64 * k < hd) ss += xe[k] * xe[k];
         ss = wave_sum(ss);
         rms = 1.0f / sqrtf(ss / (float)hd + eps);
     }
-    for (int i = lane; i < half; i += 64) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = lane + 64 * k;
+        if (i >= half) break;
         const int i0 = style == 0 ? 2 * i : i;
         const int i1 = style == 0 ? 2 * i + 1 : i + half;
-        float x0 = src[i0], x1 = src[i1];
+        float a0 = x0[k], a1 = x1[k];
         if (nw) {
-            x0 = (x0 * rms) * nw[i0];
-            x1 = (x1 * rms) * nw[i1];
+            a0 = (a0 * rms) * w0[k];
+            a1 = (a1 * rms) * w1[k];
         }
-        const float c = cr[i], s = sr[i];
-        float o0 = x0 * c - x1 * s;
-        float o1 = x1 * c + x0 * s;
+        const float c = cv[k], sn = sv[k];
+        float o0 = a0 * c - a1 * sn;
+        float o1 = a1 * c + a0 * sn;
         if (cache) {
             const uint16_t h0 = f32_to_f16_bits(o0), h1 = f32_to_f16_bits(o1);
             cache[i0] = h0;
@@ -866,43 +889,62 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) red[(pg * G + g) * HD + dsub * 8 + e] = acc[g][e];
     __syncthreads();
+    // The split's record goes out with agent-scope stores (past the per-XCD
+    // L2s), each thread waits for its own, and only then is the arrival
+    // counted (agent-scope atomic); the last block reads the records with
+    // agent-scope loads.  No cache write-back or invalidate is needed.
     float* out = a.part + ((size_t)kvh * a.max_splits + s) * G * (HD + 2);
     for (int i = tid; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
         float sum = 0.0f;
         for (int k = 0; k < PG; k++) sum += red[(k * G + g) * HD + d];
-        out[g * (HD + 2) + d] = sum;
+        st_coherent(out + g * (HD + 2) + d, sum);
     }
     if (tid < G) {
-        out[tid * (HD + 2) + HD] = ml[2 * tid];
-        out[tid * (HD + 2) + HD + 1] = ml[2 * tid + 1];
+        st_coherent(out + tid * (HD + 2) + HD, ml[2 * tid]);
+        st_coherent(out + tid * (HD + 2) + HD + 1, ml[2 * tid + 1]);
     }
 
     // the last block of this KV head merges all splits
-    __threadfence();
+    wait_all();
     __syncthreads();
-    if (tid == 0) is_last = atomicAdd(&a.done[kvh], 1u) == (unsigned)(splits - 1);
+    if (tid == 0)
+        is_last = __hip_atomic_fetch_add(&a.done[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  (unsigned)(splits - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     const float* base = a.part + (size_t)kvh * a.max_splits * G * (HD + 2);
     const size_t stride = (size_t)G * (HD + 2);
     float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int gd = tid % GD4, sg = tid / GD4;
     const int g = gd / (HD / 4), d4 = (gd % (HD / 4)) * 4;
     if (sg < SG) {
-        for (int sp = sg; sp < splits; sp += SG) {
-            const float* ps = base + sp * stride + g * (HD + 2);
-            const float ms = ps[HD], ls = ps[HD + 1];
-            const float4 os = *reinterpret_cast<const float4*>(ps + d4);
-            const float mn = fmaxf(m, ms);
-            const float fa = expf(m - mn), fb = expf(ms - mn);
-            l = l * fa + ls * fb;
-            o[0] = o[0] * fa + os.x * fb;
-            o[1] = o[1] * fa + os.y * fb;
-            o[2] = o[2] * fa + os.z * fb;
-            o[3] = o[3] * fa + os.w * fb;
-            m = mn;
+        // records sp = sg, sg + SG, ... merged in that order; the loads of a
+        // batch of kMergeB records are issued before the first is used
+        constexpr int kMergeB = 8;
+        for (int sp0 = sg; sp0 < splits; sp0 += kMergeB * SG) {
+            float ms[kMergeB], ls[kMergeB], os[kMergeB][4];
+#pragma unroll
+            for (int j = 0; j < kMergeB; j++) {
+                const int sp = min(sp0 + j * SG, splits - 1);
+                const float* ps = base + sp * stride + g * (HD + 2);
+                ms[j] = ld_coherent(ps + HD);
+                ls[j] = ld_coherent(ps + HD + 1);
+#pragma unroll
+                for (int e = 0; e < 4; e++) os[j][e] = ld_coherent(ps + d4 + e);
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeB; j++) {
+                if (sp0 + j * SG >= splits) break;
+                const float mn = fmaxf(m, ms[j]);
+                const float fa = expf(m - mn), fb = expf(ms[j] - mn);
+                l = l * fa + ls[j] * fb;
+                o[0] = o[0] * fa + os[j][0] * fb;
+                o[1] = o[1] * fa + os[j][1] * fb;
+                o[2] = o[2] * fa + os[j][2] * fb;
+                o[3] = o[3] * fa + os[j][3] * fb;
+                m = mn;
+            }
         }
     }
     __syncthreads();
@@ -926,7 +968,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
         uint16_t* dst = a.out16 + (size_t)(kvh * G + g) * HD + d4;
         for (int e = 0; e < 4; e++) dst[e] = f32_to_f16_bits(O[e] / Ls);
     }
-    if (tid == 0) atomicExch(&a.done[kvh], 0u);
+    if (tid == 0) __hip_atomic_store(&a.done[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void k_advance(mdx_state* st, int advance) {
