@@ -87,6 +87,17 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Maximum over the 64 lanes, returned to every lane (through lane 63).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));          // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp<0x4E>(v));          // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp<0x124>(v));         // row_ror:4
+    v = fmaxf(v, dpp<0x128>(v));         // row_ror:8
+    v = fmaxf(v, dpp<0x142, 0xA>(v));    // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, dpp<0x143, 0xC>(v));    // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Lanes 0..31 only (lanes 32..63 are ignored), returned to every lane.
 __device__ __forceinline__ float half_sum_dpp(float v) {
     v = row_sum16(v);

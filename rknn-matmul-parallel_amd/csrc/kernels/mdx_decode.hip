@@ -670,8 +670,12 @@ struct AttnArgs {
     uint16_t* out16;          // [nq*hd]
 };
 
+// Splits of up to kAttnChunk positions (more when L exceeds max_splits of
+// them): fewer split records to merge, and a block's tiles are requested
+// together (k_attn_decode issues its first kAttnPf tiles before anything else).
+constexpr int kAttnChunk = 64, kAttnPf = 4;
 __device__ __forceinline__ void attn_plan(int L, int max_splits, int& splits, int& chunk) {
-    int s = (L + 15) / 16;
+    int s = (L + kAttnChunk - 1) / kAttnChunk;
     if (s > max_splits) s = max_splits;
     chunk = (L + s - 1) / s;
     splits = (L + chunk - 1) / chunk;
@@ -773,15 +777,18 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
     const int sub = lane % LP, slot = lane / LP;
     const int dsub = tid % LP, pg = tid / LP;
 
-    // first K and V tiles: issue the cache loads before anything else
-    uint4 kpre = make_uint4(0, 0, 0, 0), vpre = make_uint4(0, 0, 0, 0);
-    {
-        const int pk = p0 + wave * PPW + slot;
-        if (wave * PPW + slot < n && pk < pos)
-            kpre = *reinterpret_cast<const uint4*>(a.kc + (size_t)pk * kvd + kvh * HD + sub * 8);
-        const int pv = p0 + pg;
-        if (pg < n && pv < pos)
-            vpre = *reinterpret_cast<const uint4*>(a.vc + (size_t)pv * kvd + kvh * HD + dsub * 8);
+    // the first kAttnPf K tiles and V position groups: the cache loads are
+    // issued before anything else (the newest row, pos, comes from LDS)
+    uint4 kpre[kAttnPf], vpre[kAttnPf];
+#pragma unroll
+    for (int t = 0; t < kAttnPf; t++) {
+        const int pik = t * TILE + wave * PPW + slot, piv = t * PG + pg;
+        kpre[t] = make_uint4(0, 0, 0, 0);
+        vpre[t] = make_uint4(0, 0, 0, 0);
+        if (pik < n && p0 + pik < pos)
+            kpre[t] = *reinterpret_cast<const uint4*>(a.kc + (size_t)(p0 + pik) * kvd + kvh * HD + sub * 8);
+        if (piv < n && p0 + piv < pos)
+            vpre[t] = *reinterpret_cast<const uint4*>(a.vc + (size_t)(p0 + piv) * kvd + kvh * HD + dsub * 8);
     }
 
     // QK-norm + RoPE of the G query heads (every block), and of the newest
@@ -807,8 +814,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
     }
     __syncthreads();
 
-    // scores
-    for (int t0 = 0; t0 < n; t0 += TILE) {
+    // scores: tile t0 (positions t0 .. t0 + TILE - 1 of the split)
+    auto score_tile = [&](int t0, uint4 kv) {
         const int pi = t0 + wave * PPW + slot;
         const bool act = pi < n;
         const int p = p0 + pi;
@@ -817,11 +824,6 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; e++) kf[e] = kn[sub * 8 + e];
         } else {
-            uint4 kv = kpre;
-            if (t0 > 0) {
-                kv = make_uint4(0, 0, 0, 0);
-                if (act) kv = *reinterpret_cast<const uint4*>(a.kc + (size_t)p * kvd + kvh * HD + sub * 8);
-            }
             const half2_t k01 = as_h2(kv.x), k23 = as_h2(kv.y), k45 = as_h2(kv.z), k67 = as_h2(kv.w);
             kf[0] = (float)k01.x; kf[1] = (float)k01.y; kf[2] = (float)k23.x; kf[3] = (float)k23.y;
             kf[4] = (float)k45.x; kf[5] = (float)k45.y; kf[6] = (float)k67.x; kf[7] = (float)k67.y;
@@ -832,23 +834,33 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
             float pd = qq[0] * kf[0];
 #pragma unroll
             for (int e = 1; e < 8; e++) pd = pd + qq[e] * kf[e];
-            pd = group_sum(pd, LP);
+            if constexpr (LP == 16) pd = row_sum16(pd);   // DPP within the 16-lane row
+            else pd = group_sum(pd, LP);
             if (act && sub == 0) sc[g * a.chunk_cap + pi] = pd * scale;
         }
+    };
+#pragma unroll
+    for (int t = 0; t < kAttnPf; t++)
+        if (t * TILE < n) score_tile(t * TILE, kpre[t]);
+    for (int t0 = kAttnPf * TILE; t0 < n; t0 += TILE) {
+        const int pi = t0 + wave * PPW + slot;
+        uint4 kv = make_uint4(0, 0, 0, 0);
+        if (pi < n && p0 + pi < pos) kv = *reinterpret_cast<const uint4*>(a.kc + (size_t)(p0 + pi) * kvd + kvh * HD + sub * 8);
+        score_tile(t0, kv);
     }
     __syncthreads();
 
     for (int g = wave; g < G; g += 4) {
         float m = -1e30f;
         for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[g * a.chunk_cap + i]);
-        m = wave_max(m);
+        m = wave_max_dpp(m);
         float l = 0.0f;
         for (int i = lane; i < n; i += 64) {
             const float e = expf(sc[g * a.chunk_cap + i] - m);
             sc[g * a.chunk_cap + i] = e;
             l += e;
         }
-        l = wave_sum(l);
+        l = wave_sum_dpp(l);
         if (lane == 0) {
             ml[2 * g] = m;
             ml[2 * g + 1] = l;
@@ -862,15 +874,13 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[g][e] = 0.0f;
-    for (int pi = pg; pi < n; pi += PG) {
+    auto pv_row = [&](int pi, uint4 vv) {
         const int p = p0 + pi;
         float vf[8];
         if (p == pos) {
 #pragma unroll
             for (int e = 0; e < 8; e++) vf[e] = vn[dsub * 8 + e];
         } else {
-            const uint4 vv = pi == pg ? vpre
-                                      : *reinterpret_cast<const uint4*>(a.vc + (size_t)p * kvd + kvh * HD + dsub * 8);
             const half2_t v01 = as_h2(vv.x), v23 = as_h2(vv.y), v45 = as_h2(vv.z), v67 = as_h2(vv.w);
             vf[0] = (float)v01.x; vf[1] = (float)v01.y; vf[2] = (float)v23.x; vf[3] = (float)v23.y;
             vf[4] = (float)v45.x; vf[5] = (float)v45.y; vf[6] = (float)v67.x; vf[7] = (float)v67.y;
@@ -881,7 +891,12 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[g][e] = acc[g][e] + vf[e] * pw;
         }
-    }
+    };
+#pragma unroll
+    for (int t = 0; t < kAttnPf; t++)
+        if (t * PG + pg < n) pv_row(t * PG + pg, vpre[t]);
+    for (int pi = kAttnPf * PG + pg; pi < n; pi += PG)
+        pv_row(pi, *reinterpret_cast<const uint4*>(a.vc + (size_t)(p0 + pi) * kvd + kvh * HD + dsub * 8));
     __syncthreads();   // scores no longer needed: smem is reused for the cross-group sum
     float* red = smem; // [PG][G][HD]
 #pragma unroll
@@ -921,7 +936,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
     if (sg < SG) {
         // records sp = sg, sg + SG, ... merged in that order; the loads of a
         // batch of kMergeB records are issued before the first is used
-        constexpr int kMergeB = 8;
+        constexpr int kMergeB = 12;
         for (int sp0 = sg; sp0 < splits; sp0 += kMergeB * SG) {
             float ms[kMergeB], ls[kMergeB], os[kMergeB][4];
 #pragma unroll
@@ -1111,7 +1126,7 @@ int mdx_launch_attn_decode(const mdx_state* state, const float* qkv, const float
     a.nkv = nkv;
     a.max_splits = max_splits;
     a.chunk_cap = (max_seq + max_splits - 1) / max_splits;
-    if (a.chunk_cap < 16) a.chunk_cap = 16;
+    if (a.chunk_cap < kAttnChunk) a.chunk_cap = kAttnChunk;
     a.part = (float*)scratch;
     a.done = (unsigned int*)((char*)scratch + (size_t)nq * max_splits * (hd + 2) * 4);
     a.out16 = attn_out16;
