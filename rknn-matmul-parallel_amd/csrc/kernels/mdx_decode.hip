@@ -904,6 +904,17 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) red[(pg * G + g) * HD + dsub * 8 + e] = acc[g][e];
     __syncthreads();
+    if (splits == 1) {
+        // the only split: its sums are final (the merge of one record
+        // computes the same quotient), so no record, arrival or merge
+        for (int i = tid; i < G * HD; i += 256) {
+            const int g = i / HD, d = i % HD;
+            float sum = 0.0f;
+            for (int k = 0; k < PG; k++) sum += red[(k * G + g) * HD + d];
+            a.out16[(size_t)(kvh * G + g) * HD + d] = f32_to_f16_bits(sum / ml[2 * g + 1]);
+        }
+        return;
+    }
     // The split's record goes out with agent-scope stores (past the per-XCD
     // L2s), each thread waits for its own, and only then is the arrival
     // counted (agent-scope atomic); the last block reads the records with
