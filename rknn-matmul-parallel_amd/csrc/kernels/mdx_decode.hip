@@ -26,6 +26,8 @@ using namespace mdx;
 
 namespace {
 
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
 enum XMode { XM_NORM = 0, XM_F16 = 1, XM_F32 = 2, XM_EMBED = 3 };
 enum Epi { EP_STORE = 0, EP_ADD = 1, EP_SWIGLU = 2, EP_LOGITS = 3 };
 // KF16/KI8/KI4: fp16 activations (the NPU input).  KF32X: fp32 rows with fp32
@@ -665,7 +667,7 @@ struct AttnArgs {
     int nkv;
     int max_splits;
     int chunk_cap;
-    float* part;              // [nkv][max_splits][G][hd + 2]
+    float* part;              // [nkv][max_splits][G][hd + 4]
     unsigned int* done;       // [nkv], zero between launches
     uint16_t* out16;          // [nq*hd]
 };
@@ -915,20 +917,30 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
         }
         return;
     }
-    // The split's record goes out with agent-scope stores (past the per-XCD
-    // L2s), each thread waits for its own, and only then is the arrival
-    // counted (agent-scope atomic); the last block reads the records with
-    // agent-scope loads.  No cache write-back or invalidate is needed.
-    float* out = a.part + ((size_t)kvh * a.max_splits + s) * G * (HD + 2);
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        float sum = 0.0f;
-        for (int k = 0; k < PG; k++) sum += red[(k * G + g) * HD + d];
-        st_coherent(out + g * (HD + 2) + d, sum);
+    // The split's record ([G][HD + 4] floats: the HD sums, then m, l and two
+    // unused words, so every head starts on 16 bytes) goes out as 16-byte
+    // stores with the sc1 policy (what an agent-scope atomic store compiles
+    // to: past the per-XCD L2s); each thread waits for its own stores, and
+    // only then is the arrival counted (agent-scope atomic).  The last block
+    // reads the records with 16-byte sc1 loads.  No cache write-back or
+    // invalidate is needed.
+    constexpr int RH = HD + 4;              // floats per head in a record
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(a.part, (short)0, 0x7fffffff, 0x00020000);
+    const unsigned rec0 = (unsigned)(((size_t)kvh * a.max_splits + s) * G * RH * 4);
+    for (int i4 = tid; i4 < G * HD / 4; i4 += 256) {
+        const int g = (4 * i4) / HD, d = (4 * i4) % HD;
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < PG; k++) {
+            const float4 r = *reinterpret_cast<const float4*>(red + (k * G + g) * HD + d);
+            sum.x += r.x; sum.y += r.y; sum.z += r.z; sum.w += r.w;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, sum), prs,
+                                               rec0 + (unsigned)(g * RH + d) * 4, 0, 16);
     }
     if (tid < G) {
-        st_coherent(out + tid * (HD + 2) + HD, ml[2 * tid]);
-        st_coherent(out + tid * (HD + 2) + HD + 1, ml[2 * tid + 1]);
+        const float4 t4 = make_float4(ml[2 * tid], ml[2 * tid + 1], 0.f, 0.f);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, t4), prs,
+                                               rec0 + (unsigned)(tid * RH + HD) * 4, 0, 16);
     }
 
     // the last block of this KV head merges all splits
@@ -939,8 +951,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
                   (unsigned)(splits - 1);
     __syncthreads();
     if (!is_last) return;
-    const float* base = a.part + (size_t)kvh * a.max_splits * G * (HD + 2);
-    const size_t stride = (size_t)G * (HD + 2);
+    const unsigned base = (unsigned)((size_t)kvh * a.max_splits * G * RH * 4);
+    const unsigned stride = (unsigned)(G * RH * 4);
     float m = -INFINITY, l = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int gd = tid % GD4, sg = tid / GD4;
     const int g = gd / (HD / 4), d4 = (gd % (HD / 4)) * 4;
@@ -949,26 +961,25 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
         // batch of kMergeB records are issued before the first is used
         constexpr int kMergeB = 12;
         for (int sp0 = sg; sp0 < splits; sp0 += kMergeB * SG) {
-            float ms[kMergeB], ls[kMergeB], os[kMergeB][4];
+            u32x4_t ml4[kMergeB], os4[kMergeB];
 #pragma unroll
             for (int j = 0; j < kMergeB; j++) {
                 const int sp = min(sp0 + j * SG, splits - 1);
-                const float* ps = base + sp * stride + g * (HD + 2);
-                ms[j] = ld_coherent(ps + HD);
-                ls[j] = ld_coherent(ps + HD + 1);
-#pragma unroll
-                for (int e = 0; e < 4; e++) os[j][e] = ld_coherent(ps + d4 + e);
+                const unsigned ps = base + (unsigned)sp * stride + (unsigned)(g * RH) * 4;
+                ml4[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, ps + HD * 4, 0, 16);
+                os4[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, ps + (unsigned)d4 * 4, 0, 16);
             }
 #pragma unroll
             for (int j = 0; j < kMergeB; j++) {
                 if (sp0 + j * SG >= splits) break;
-                const float mn = fmaxf(m, ms[j]);
-                const float fa = expf(m - mn), fb = expf(ms[j] - mn);
-                l = l * fa + ls[j] * fb;
-                o[0] = o[0] * fa + os[j][0] * fb;
-                o[1] = o[1] * fa + os[j][1] * fb;
-                o[2] = o[2] * fa + os[j][2] * fb;
-                o[3] = o[3] * fa + os[j][3] * fb;
+                const float msj = __uint_as_float(ml4[j].x), lsj = __uint_as_float(ml4[j].y);
+                const float mn = fmaxf(m, msj);
+                const float fa = expf(m - mn), fb = expf(msj - mn);
+                l = l * fa + lsj * fb;
+                o[0] = o[0] * fa + __uint_as_float(os4[j].x) * fb;
+                o[1] = o[1] * fa + __uint_as_float(os4[j].y) * fb;
+                o[2] = o[2] * fa + __uint_as_float(os4[j].z) * fb;
+                o[3] = o[3] * fa + __uint_as_float(os4[j].w) * fb;
                 m = mn;
             }
         }
@@ -1113,7 +1124,7 @@ int mdx_attn_max_splits(int max_seq) {
 }
 
 size_t mdx_attn_decode_scratch_bytes(int nq, int nkv, int hd, int max_splits) {
-    return (size_t)nq * max_splits * (hd + 2) * 4 + (size_t)nkv * 4;
+    return (size_t)nq * max_splits * (hd + 4) * 4 + (size_t)nkv * 4;
 }
 
 int mdx_launch_attn_decode(const mdx_state* state, const float* qkv, const float* q_norm,
@@ -1139,7 +1150,7 @@ int mdx_launch_attn_decode(const mdx_state* state, const float* qkv, const float
     a.chunk_cap = (max_seq + max_splits - 1) / max_splits;
     if (a.chunk_cap < kAttnChunk) a.chunk_cap = kAttnChunk;
     a.part = (float*)scratch;
-    a.done = (unsigned int*)((char*)scratch + (size_t)nq * max_splits * (hd + 2) * 4);
+    a.done = (unsigned int*)((char*)scratch + (size_t)nq * max_splits * (hd + 4) * 4);
     a.out16 = attn_out16;
     const int LP = hd / 8;
     const int PG = 256 / LP;
