@@ -594,7 +594,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         // us/token, tokens unchanged; the same code measured +0.7 us with fp16
         // and +1.8 us with int8 layers at KV 512, so those keep the form below)
         constexpr bool kLean = KIND == MDX_W_I4;
-        const float sclA = Ly.sqkv && (!kLean || wave == 0) ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
+        float sclA = Ly.sqkv && (!kLean || wave == 0) ? Ly.sqkv[qkv_row0 + (t & 15)] : 1.0f;
         if (l > 0) {
             const int wb = W_HD + (b % NREP) * (2 * D) + 8 * t;
             int wd[2] = {wb, wb + 4};
@@ -647,7 +647,12 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         rm_dot<KIND, 16, D>(wA, xs4, red, t);
-        if constexpr (kLateKV) load_kv(kr, vr, 0);
+        if constexpr (kLateKV) {
+            // the column scale must be in a register before the K/V requests
+            // go out: a wait for it placed after them also waits for them
+            asm volatile("" : "+v"(sclA));
+            load_kv(kr, vr, 0);
+        }
         __syncthreads();
         if (wave == 0) {
             // lanes 0..15 hold rows s*16 + lane; even lanes store two rows in one
