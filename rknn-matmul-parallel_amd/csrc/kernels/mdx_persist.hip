@@ -579,7 +579,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 
         // ================= A: RMSNorm + qkv =================
         MDX_TRACE(16 * l + 0);
-        const float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
+        float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
         // stage B inputs that do not depend on this step's activations
         const float rc = a.cos_t[(size_t)pos * (HD / 2) + lane];
         const float rsn = a.sin_t[(size_t)pos * (HD / 2) + lane];
@@ -635,7 +635,13 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         // 561.5 -> 556 us/token, int8 at KV 512 unchanged); fp16 layers here
         // (after the GEMV: +11.5 us at KV 512)
         constexpr bool kLateKV = KIND != MDX_W_F16;
-        if constexpr (!kLateKV) load_kv(kr, vr, 0);
+        if constexpr (!kLateKV) {
+            // the norm weights and the column scale must be in registers before
+            // the K/V requests go out: a wait for them placed after those
+            // requests also waits for the whole K/V round
+            asm volatile("" : "+v"(nwA.x), "+v"(nwA.y), "+v"(nwA.z), "+v"(nwA.w), "+v"(sclA));
+            load_kv(kr, vr, 0);
+        }
         uint4 wD[SD::NW];
         cm_load<KIND, 4, QD>(wD, Ly.wo, 4 * b, t);
         MDX_TRACE(16 * l + 1);
