@@ -579,7 +579,7 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
 
         // ================= A: RMSNorm + qkv =================
         MDX_TRACE(16 * l + 0);
-        float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
+        const float4 nwA = reinterpret_cast<const float4*>(Ly.in_norm)[t];
         // stage B inputs that do not depend on this step's activations
         const float rc = a.cos_t[(size_t)pos * (HD / 2) + lane];
         const float rsn = a.sin_t[(size_t)pos * (HD / 2) + lane];
@@ -630,18 +630,6 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
                 }
             }
         };
-        // the first K/V round: for int8 and int4 layers after the qkv GEMV
-        // (below), which otherwise waits for part of it (W4A16 at KV 4096
-        // 561.5 -> 556 us/token, int8 at KV 512 unchanged); fp16 layers here
-        // (after the GEMV: +11.5 us at KV 512)
-        constexpr bool kLateKV = KIND != MDX_W_F16;
-        if constexpr (!kLateKV) {
-            // the norm weights and the column scale must be in registers before
-            // the K/V requests go out: a wait for them placed after those
-            // requests also waits for the whole K/V round
-            asm volatile("" : "+v"(nwA.x), "+v"(nwA.y), "+v"(nwA.z), "+v"(nwA.w), "+v"(sclA));
-            load_kv(kr, vr, 0);
-        }
         uint4 wD[SD::NW];
         cm_load<KIND, 4, QD>(wD, Ly.wo, 4 * b, t);
         MDX_TRACE(16 * l + 1);
@@ -653,12 +641,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         rm_dot<KIND, 16, D>(wA, xs4, red, t);
-        if constexpr (kLateKV) {
-            // the column scale must be in a register before the K/V requests
-            // go out: a wait for it placed after them also waits for them
-            asm volatile("" : "+v"(sclA));
-            load_kv(kr, vr, 0);
-        }
+        // the first K/V round goes out after the qkv GEMV, which otherwise
+        // waits for part of it (fp16 at KV 4096 556.5 -> 550.7, W4A16 at KV
+        // 4096 561.5 -> 556 us/token). The column scale is forced into a
+        // register first: loads complete in issue order, so a wait for it
+        // placed after these requests would wait for the whole round and hold
+        // back the qkv store (int8 KV 512 407.4 -> 404.5 us/token)
+        asm volatile("" : "+v"(sclA));
+        load_kv(kr, vr, 0);
         __syncthreads();
         if (wave == 0) {
             // lanes 0..15 hold rows s*16 + lane; even lanes store two rows in one
