@@ -660,12 +660,14 @@ __global__ __launch_bounds__(NT) void k_persist_step(PArgs a) {
         }
         __syncthreads();
         rm_dot<KIND, 16, D>(wA, xs4, red, t);
-        // the first K/V round goes out after the qkv GEMV, which otherwise
-        // waits for part of it (fp16 at KV 4096 556.5 -> 550.7, W4A16 at KV
-        // 4096 561.5 -> 556 us/token). The column scale is forced into a
-        // register first: loads complete in issue order, so a wait for it
-        // placed after these requests would wait for the whole round and hold
-        // back the qkv store (int8 KV 512 407.4 -> 404.5 us/token)
+        // Layer 0, and fp16 layers with a streamed cache, request their first
+        // K/V round here (the others did at the end of the previous layer's
+        // gate|up stage): after the qkv GEMV, which otherwise waits for part
+        // of it (fp16 at KV 4096 556.5 -> 550.7, W4A16 at KV 4096 561.5 -> 556
+        // us/token). The column scale is forced into a register first: loads
+        // complete in issue order, so a wait for it placed after later
+        // requests would wait for them too and hold back the qkv store (int8
+        // KV 512 407.4 -> 404.5 us/token)
         asm volatile("" : "+v"(sclA));
         if (!early_kv || l == 0) load_kv(kr, vr, 0);
         __syncthreads();
