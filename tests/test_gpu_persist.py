@@ -127,7 +127,10 @@ def test_local_exchange_is_bit_identical(mdx, gpu, oracle_lib, models, quant, n_
 def test_kv_load_policy_is_bit_identical(mdx, gpu, oracle_lib, models, n_pos):
     """The K/V rows read with ordinary or with non-temporal loads (the policy
     the host picks by cache size) give the same bits: logits, token and the
-    appended K/V row, over three steps."""
+    appended K/V row, over three steps. With fp16 layers the policy also moves
+    the first K/V round of each layer: requested at the end of the previous
+    layer's gate|up stage (ordinary loads) or in the layer's own qkv stage
+    (non-temporal loads)."""
     cfg, get = models
     path = get(0)
     runs = []
