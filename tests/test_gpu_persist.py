@@ -134,22 +134,25 @@ def test_kv_load_policy_is_bit_identical(mdx, gpu, oracle_lib, models, n_pos):
     cfg, get = models
     path = get(0)
     runs = []
-    for mode in (0, 1):
+    # ordinary loads, non-temporal loads, and the policy switched between the
+    # steps of one decoder (each launch decides on its own)
+    for modes in ((0, 0, 0), (1, 1, 1), (0, 1, 0)):
         g, _ = _pair(mdx, oracle_lib, cfg, path, 0)
-        g.force_kv_stream(mode)
         g.kv_fill_normal(n_pos, 91)
         out = []
         tok = 1234
-        for _ in range(3):
+        for mode in modes:
+            g.force_kv_stream(mode)
             tok, lg = g.step(tok)
             out.append((tok, lg.copy()))
         k, v = g.kv_read(1, n_pos, 3)
         runs.append((out, k.copy(), v.copy()))
         g.close()
-    (a, ka, va), (b, kb, vb) = runs
-    for (ta, la), (tb, lb) in zip(a, b):
-        assert ta == tb and np.array_equal(la, lb)
-    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    a, ka, va = runs[0]
+    for b, kb, vb in runs[1:]:
+        for (ta, la), (tb, lb) in zip(a, b):
+            assert ta == tb and np.array_equal(la, lb)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
 
 
 @pytest.mark.parametrize("quant", [0, 1, 2])
