@@ -703,8 +703,18 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const mdx_state* st, const
     const int kvd = nkv * HD;
     const int pl = tid / LP, dl = tid % LP;
     const float scale = 1.0f / sqrtf((float)HD);
-    // the first round's K/V rows are requested before q is staged, so the
-    // two loads overlap (measured: -0.4 us per layer at M = 60)
+    // q is requested first and the first round's K/V rows right after it, so
+    // the loads overlap (-0.4 us per layer at M = 60 against staging q
+    // first) and, loads completing in issue order, staging q into LDS waits
+    // for q alone while the K/V rows are still in flight (M = 60 INT8 prefill
+    // 1.0934 -> 1.0874 ms against requesting the K/V rows first)
+    constexpr int QPT = (G * HD + 255) / 256;
+    float qv[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int i = tid + 256 * k;
+        qv[k] = i < G * HD ? q[(size_t)t * nq * HD + (size_t)kvh * G * HD + i] : 0.0f;
+    }
     uint4 kk[PP], vv[PP];
     auto load_round = [&](int r0) {
 #pragma unroll
@@ -716,7 +726,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const mdx_state* st, const
         }
     };
     load_round(0);
-    for (int i = tid; i < G * HD; i += 256) qs[i] = q[(size_t)t * nq * HD + (size_t)kvh * G * HD + i];
+#pragma unroll
+    for (int k = 0; k < QPT; k++)
+        if (tid + 256 * k < G * HD) qs[tid + 256 * k] = qv[k];
     __syncthreads();
     float qr[G][8];
 #pragma unroll
