@@ -115,10 +115,49 @@ __device__ __forceinline__ float chunk_dot(uint4 w, const uint4* xs, int j, floa
 // wait on each element for every earlier load, the weights included.
 constexpr int kXV = 2;
 
+// The row that supplies x (the embedding row of the current token in
+// XM_EMBED mode, unless the embedding was uploaded).
+__device__ __forceinline__ const float* x_source(const GemvArgs& a) {
+    const float* src = a.xf32;
+    if (a.xmode == XM_EMBED && a.st_in->mode != 1) {
+        int tok = a.st_in->token;
+        tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
+        src = a.emb_table + (size_t)tok * a.K;
+    }
+    return src;
+}
+
+// The first batch of build_x's loads, issued on its own so that a kernel can
+// request x before its weights: loads complete in issue order, so staging x
+// then waits for x alone while the weights are still arriving.
+struct XFirst {
+    float4 v[kXV], g[kXV];
+    uint2 h[kXV];
+};
+__device__ __forceinline__ void build_x_first(const GemvArgs& a, XFirst& f) {
+    const int tid = threadIdx.x, nt = blockDim.x, nv = a.K / 4;
+    if (a.xmode == XM_F16) {
+        const uint2* x16 = reinterpret_cast<const uint2*>(a.x16);
+#pragma unroll
+        for (int i = 0; i < kXV; i++) f.h[i] = x16[min(tid + i * nt, nv - 1)];
+        return;
+    }
+    const float4* s4 = reinterpret_cast<const float4*>(x_source(a));
+#pragma unroll
+    for (int i = 0; i < kXV; i++) f.v[i] = s4[min(tid + i * nt, nv - 1)];
+    if (a.xmode == XM_NORM || a.xmode == XM_EMBED) {
+        const float4* g4 = reinterpret_cast<const float4*>(a.norm_w);
+#pragma unroll
+        for (int i = 0; i < kXV; i++) f.g[i] = g4[min(tid + i * nt, nv - 1)];
+    }
+}
+
 // Builds the activation vector in LDS: fp16 for the NPU-style kinds, fp32 for
 // the CPU-GEMV kinds.  XM_NORM / XM_EMBED apply the reference RMSNorm first.
+// With `first`, the first batch comes from build_x_first instead of new loads.
 template <bool XF32>
-__device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* red) {
+__device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* red,
+                                        const XFirst* first = nullptr) {
     const int tid = threadIdx.x, nt = blockDim.x;
     const int K = a.K, nv = K / 4, step = kXV * nt;
     float4* xs32 = reinterpret_cast<float4*>(xs_raw);
@@ -128,7 +167,7 @@ __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* 
         for (int q0 = tid; q0 < nv; q0 += step) {
             uint2 h[kXV];
 #pragma unroll
-            for (int i = 0; i < kXV; i++) h[i] = x16[min(q0 + i * nt, nv - 1)];
+            for (int i = 0; i < kXV; i++) h[i] = first && q0 == tid ? first->h[i] : x16[min(q0 + i * nt, nv - 1)];
 #pragma unroll
             for (int i = 0; i < kXV; i++) {
                 const int q = q0 + i * nt;
@@ -142,23 +181,26 @@ __device__ __forceinline__ void build_x(const GemvArgs& a, void* xs_raw, float* 
         __syncthreads();
         return;
     }
-    const float* src = a.xf32;
+    const float* src = x_source(a);
     const bool embed = a.xmode == XM_EMBED;
-    if (embed && a.st_in->mode != 1) {
-        int tok = a.st_in->token;
-        tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);
-        src = a.emb_table + (size_t)tok * K;
-    }
     const bool norm = a.xmode == XM_NORM || embed;
     const bool copy = embed && blockIdx.x == 0;
     const float4* s4 = reinterpret_cast<const float4*>(src);
     const float4* g4 = reinterpret_cast<const float4*>(a.norm_w);
     float4 v[kXV], g[kXV];
+    if (first) {
 #pragma unroll
-    for (int i = 0; i < kXV; i++) v[i] = s4[min(tid + i * nt, nv - 1)];
-    if (norm) {
+        for (int i = 0; i < kXV; i++) {
+            v[i] = first->v[i];
+            g[i] = first->g[i];
+        }
+    } else {
 #pragma unroll
-        for (int i = 0; i < kXV; i++) g[i] = g4[min(tid + i * nt, nv - 1)];
+        for (int i = 0; i < kXV; i++) v[i] = s4[min(tid + i * nt, nv - 1)];
+        if (norm) {
+#pragma unroll
+            for (int i = 0; i < kXV; i++) g[i] = g4[min(tid + i * nt, nv - 1)];
+        }
     }
     float rms = 1.0f;
     if (norm) {
@@ -390,8 +432,13 @@ __global__ __launch_bounds__(256) void k_gemv_once(GemvArgs a) {
     RowSet<KIND, RW, U> rs;
     uint4 wv[RW][U];
     rs.init(a, blockIdx.x, wave);
+    // x first, then the weights: staging x waits for x alone while the
+    // weights arrive (config 2's four launches 17.51 -> 17.14 us, the INT8
+    // 1 x 1024 x 4096 tile 3.02 -> 2.97 us)
+    XFirst xf;
+    build_x_first(a, xf);
     rs.load(a, row_bytes, nchunks, 0, lane, wv);
-    build_x<T::XF32>(a, xs, red);
+    build_x<T::XF32>(a, xs, red, &xf);
     float y[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
